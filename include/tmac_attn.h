@@ -1,0 +1,182 @@
+/*
+ * tmac_attn.h -- C ABI of the MI355X (gfx950) attention hot path of
+ * liuwantao3/tmac_gguf.cpp: GQA decode attention over the fp32 KV cache,
+ * RoPE, and the KV-cache row write.
+ *
+ * The reference engine calls three Metal dispatch helpers from its per-layer
+ * loop (tmac_gguf.cpp:1562-1568), bracketed by metal_batch_begin/end:
+ *
+ *   attention_op(ctx, Q, K_cache, V_cache, output, n_head, n_kv_head, head_dim, past_len)
+ *                                                    metal_backend.hpp:413-453
+ *   rope_op(ctx, data, n_heads, head_dim, pos, base) metal_backend.hpp:381-396
+ *   elem_op(ctx, 2, cache_row, src, dim)             metal_backend.hpp:354-379 (op 2 = copy)
+ *
+ * This header exports the same three operations with the same argument
+ * meaning, plus context lifecycle, step capture (hipGraph, the analogue of the
+ * one command buffer per decode step), a fused per-layer entry point and the
+ * batched / ragged-split-KV extensions.
+ *
+ * Conventions (all entry points):
+ *  - Buffers are DEVICE pointers owned by the caller (allocate them with
+ *    tmac_malloc or hipMalloc).  The library never frees caller memory.
+ *  - Every call returns int status: 0 (TMAC_OK) or a TMAC_ERR_* code.  Shape
+ *    and pointer checks run on the host before any launch; a rejected call
+ *    launches nothing.  HIP runtime failures return TMAC_ERR_HIP_BASE + hipError_t.
+ *  - Calls are stream-ordered and asynchronous; `stream` is a hipStream_t
+ *    (NULL = the null stream).
+ *  - A context is used from one host thread at a time, and its launches must
+ *    not overlap on several streams (they share the split-KV workspace).
+ *  - Cache layout is the reference's: one row per position, row =
+ *    [n_kv_head][head_dim] fp32 (tmac_gguf.cpp:200-201).  head_dim must be 64,
+ *    as in the reference's flash kernel (kernel_flash_attn.metal:18).
+ *    Query head h reads kv head h / (n_head / n_kv_head) (tmac_gguf.cpp:1099).
+ */
+#ifndef TMAC_ATTN_H
+#define TMAC_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMAC_ATTN_ABI_VERSION 1
+
+enum tmac_status {
+    TMAC_OK = 0,
+    TMAC_ERR_INVALID_ARG = 1,     /* bad shape or value (negative past_len, n_head % n_kv_head, ...) */
+    TMAC_ERR_NULL_POINTER = 2,
+    TMAC_ERR_MISALIGNED = 3,      /* q/k/v/out/cache rows must be 16-byte aligned */
+    TMAC_ERR_UNSUPPORTED = 4,     /* head_dim != 64, unsupported GQA group, elem_op op != 2 */
+    TMAC_ERR_CAPACITY = 5,        /* position beyond the cache / RoPE table / workspace */
+    TMAC_ERR_NOT_INITIALIZED = 6,
+    TMAC_ERR_CAPTURE = 7,         /* needs an allocation while the stream is being captured */
+    TMAC_ERR_DEVICE_FAULT = 8,    /* a kernel reported a bad device-side position */
+    TMAC_ERR_HIP_BASE = 1000      /* TMAC_ERR_HIP_BASE + hipError_t */
+};
+
+typedef struct tmac_context tmac_context;
+typedef struct tmac_graph tmac_graph;
+typedef void* tmac_stream;  /* hipStream_t */
+
+/* Human-readable text for a status code (static storage). */
+const char* tmac_status_string(int status);
+/* Detail of the last error reported through this context (thread-unsafe, like the context). */
+const char* tmac_last_error(const tmac_context* ctx);
+int tmac_abi_version(void);
+
+/* ---- lifecycle: replaces metal_backend::init / shutdown (metal_backend.cpp:21-89, .hpp:519-520) ----
+ * Loads the gfx950 code object embedded in this library (hipModuleLoadData)
+ * on `device`, resolves every kernel, and allocates the split-KV workspace.
+ * Fails with TMAC_ERR_HIP_BASE+... when no device or no gfx950 is present. */
+int tmac_init(tmac_context** ctx, int device);
+int tmac_shutdown(tmac_context* ctx);
+
+/* ---- the reference's three per-layer dispatches ---- */
+
+/* attention_op, metal_backend.hpp:413-453 / tmac_gguf.cpp:1093-1128.
+ * q [n_head][64] (already rotated), k_cache/v_cache = row 0 of the layer
+ * cache, out [n_head][64].  Attends rows 0..past_len inclusive. */
+int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
+                      const float* v_cache, float* out, int n_head, int n_kv_head, int head_dim,
+                      int past_len);
+
+/* rope_op, metal_backend.hpp:381-396 / tmac_gguf.cpp:990-1016: rotates
+ * n_heads heads of `data` in place at position `pos` with frequency base
+ * `base` (GPT-J adjacent pairs).  cos/sin of pos*theta come from a table the
+ * context builds on the host with the platform libm (tmac_rope_prepare). */
+int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads, int head_dim,
+                 int pos, float base);
+
+/* elem_op, metal_backend.hpp:354-379.  Only op 2 (cache write:
+ * data[i] = aux[i], i < dim; tmac_gguf.cpp:1090-1091) is on this path; op 0
+ * (add) and op 1 (silu*up) return TMAC_ERR_UNSUPPORTED. */
+int tmac_elem_op(tmac_context* ctx, tmac_stream stream, int op, float* data, const float* aux, int dim);
+
+/* ---- fused per-layer step (one launch replaces rope_op x2 + elem_op(2) x2 + attention_op,
+ *      tmac_gguf.cpp:1562-1568) ----
+ * Rotates q and k_new at `pos`, writes k (rotated) and v_new to row `pos` of
+ * the layer cache, and attends rows 0..pos.  q/k_new/v_new are read only
+ * (the rotated q is not written back).  `capacity` = rows in the layer cache. */
+int tmac_layer_attention(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_new,
+                         const float* v_new, float* k_cache, float* v_cache, float* out, int n_head,
+                         int n_kv_head, int head_dim, int pos, int capacity, float base);
+/* Same, with the position read on the device from *pos_dev at run time, so a
+ * captured step graph can be replayed for successive positions.  An
+ * out-of-range *pos_dev makes the kernel skip its work and raise the device
+ * error word (see tmac_check_device_error). */
+int tmac_layer_attention_devpos(tmac_context* ctx, tmac_stream stream, const float* q,
+                                const float* k_new, const float* v_new, float* k_cache,
+                                float* v_cache, float* out, int n_head, int n_kv_head, int head_dim,
+                                const int* pos_dev, int capacity, float base);
+/* *pos_dev = value (add = 0) or *pos_dev += value (add = 1), as a kernel (graph safe). */
+int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add);
+
+/* Builds (or extends) the cos/sin table for (head_dim, base) to cover
+ * positions [0, n_pos).  Synchronous; must not be called during capture.
+ * rope_op / layer_attention build it on first use when not capturing. */
+int tmac_rope_prepare(tmac_context* ctx, int head_dim, float base, int n_pos);
+
+/* ---- batched decode (extensions; no counterpart in the single-sequence reference) ----
+ * Sequence s reads cache rows starting at k + s*seq_stride*row (row = n_kv_head*64
+ * floats) and attends its first n_pos rows; q/out are [n_seq][n_head][64]. */
+int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const float* q,
+                                  const float* k, const float* v, float* out, int n_seq,
+                                  int n_head, int n_kv_head, int head_dim, int n_pos,
+                                  int64_t seq_stride);
+/* Ragged split-KV decode over a packed pool: sequence s attends rows
+ * [offsets[s], offsets[s] + lengths[s]) (DEVICE arrays).  max_len bounds every
+ * length (it sizes the grid); longer sequences are an error the caller must
+ * avoid.  A sequence of length 0 produces a zero output. */
+int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const float* q,
+                                 const float* k_pool, const float* v_pool, const int64_t* offsets,
+                                 const int32_t* lengths, float* out, int n_seq, int n_head,
+                                 int n_kv_head, int head_dim, int max_len);
+
+/* ---- tuning / introspection ---- */
+enum tmac_option {
+    TMAC_OPT_SPLIT_LEN = 1,   /* rows per workgroup; 0 = automatic (default) */
+    TMAC_OPT_TARGET_GROUPS = 2 /* workgroups the automatic split aims for; 0 = 2 per CU */
+};
+int tmac_set_option(tmac_context* ctx, int option, int64_t value);
+/* Rows per workgroup the next decode with this shape would use. */
+int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_kv_head, int* split_len,
+                     int* n_splits);
+/* Reads and clears the device error word (bit 0: bad device-side position, bit 1: ragged length above max_len).
+ * Synchronizes the context's device. Returns TMAC_ERR_DEVICE_FAULT if set. */
+int tmac_check_device_error(tmac_context* ctx);
+
+/* ---- step capture: the analogue of metal_batch_begin / metal_batch_end
+ *      (metal_backend.hpp:114-122, 176-190), one hipGraph per decode step ---- */
+int tmac_step_begin(tmac_context* ctx, tmac_stream stream);
+/* Ends capture.  *graph == NULL: instantiates a new executable graph.
+ * *graph != NULL: updates it in place (hipGraphExecUpdate) and re-instantiates
+ * only if the topology changed. */
+int tmac_step_end(tmac_context* ctx, tmac_stream stream, tmac_graph** graph);
+int tmac_graph_launch(tmac_context* ctx, tmac_graph* graph, tmac_stream stream);
+int tmac_graph_destroy(tmac_context* ctx, tmac_graph* graph);
+
+/* ---- device memory, streams and events (for callers without their own HIP plumbing) ---- */
+int tmac_malloc(tmac_context* ctx, void** ptr, size_t bytes);
+int tmac_free(tmac_context* ctx, void* ptr);
+int tmac_memcpy_h2d(tmac_context* ctx, tmac_stream stream, void* dst, const void* src, size_t bytes);
+int tmac_memcpy_d2h(tmac_context* ctx, tmac_stream stream, void* dst, const void* src, size_t bytes);
+int tmac_memcpy_d2d(tmac_context* ctx, tmac_stream stream, void* dst, const void* src, size_t bytes);
+int tmac_memset(tmac_context* ctx, tmac_stream stream, void* dst, int value, size_t bytes);
+int tmac_stream_create(tmac_context* ctx, tmac_stream* stream);
+int tmac_stream_destroy(tmac_context* ctx, tmac_stream stream);
+int tmac_stream_synchronize(tmac_context* ctx, tmac_stream stream);
+int tmac_device_synchronize(tmac_context* ctx);
+typedef void* tmac_event;   /* hipEvent_t */
+int tmac_event_create(tmac_context* ctx, tmac_event* ev);
+int tmac_event_destroy(tmac_context* ctx, tmac_event ev);
+int tmac_event_record(tmac_context* ctx, tmac_event ev, tmac_stream stream);
+int tmac_event_elapsed_ms(tmac_context* ctx, tmac_event start, tmac_event stop, float* ms);
+/* Device facts: compute units, HBM bus width etc. are in the returned text. */
+int tmac_device_info(tmac_context* ctx, char* buf, size_t buf_len, int* n_cu);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

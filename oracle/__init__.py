@@ -1,0 +1,187 @@
+"""CPU oracle for the attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+numpy/ctypes front end of ``oracle/tmac_oracle.c``, the C restatement of the
+reference's CPU path (liuwantao3/tmac_gguf.cpp):
+
+* ``rope``            -- tmac_gguf.cpp:990-1016 (apply_rope)
+* ``cache_write``     -- tmac_gguf.cpp:1090-1091
+* ``attention``       -- tmac_gguf.cpp:1093-1128
+* ``layer_step``      -- tmac_gguf.cpp:1085-1128 (rope -> cache write -> attention)
+* ``attention_ragged``/``prefill`` -- the same per-head loop over many sequences
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
+may import this module.  It is the checker, never the thing measured or shipped:
+the product (``libtmac_attn.so``) has no CPU fallback and never loads it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+PARITY_LIB = os.path.join(LIB_DIR, "libtmac_oracle.so")
+TIMING_LIB = os.path.join(LIB_DIR, "libtmac_oracle_o3.so")
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I64 = ctypes.POINTER(ctypes.c_int64)
+_I32 = ctypes.POINTER(ctypes.c_int32)
+_libs: dict[str, ctypes.CDLL] = {}
+
+
+def build(force: bool = False) -> None:
+    """Compile the oracle with its Makefile (gcc; runs anywhere)."""
+    args = ["make", "-s", "-C", HERE]
+    if force:
+        args.insert(1, "-B")
+    subprocess.run(args, check=True)
+
+
+def _load(path: str) -> ctypes.CDLL:
+    if path in _libs:
+        return _libs[path]
+    if not os.path.exists(path):
+        build()
+    lib = ctypes.CDLL(path)
+    lib.tmac_fill_normal.argtypes = [ctypes.c_uint64, _F, ctypes.c_size_t]
+    lib.tmac_fill_normal.restype = None
+    lib.tmac_splitmix64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    lib.tmac_splitmix64.restype = ctypes.c_uint64
+    lib.oracle_rope_heads.argtypes = [_F, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+    lib.oracle_rope_heads.restype = None
+    lib.oracle_rope_theta.argtypes = [_F, ctypes.c_int, ctypes.c_float]
+    lib.oracle_rope_theta.restype = None
+    lib.oracle_cache_write.argtypes = [_F, _F, ctypes.c_int]
+    lib.oracle_cache_write.restype = None
+    lib.oracle_attention.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 4
+    lib.oracle_attention.restype = ctypes.c_int
+    lib.oracle_layer_step.argtypes = [_F, _F, _F, _F, _F, _F] + [ctypes.c_int] * 4 + [ctypes.c_float]
+    lib.oracle_layer_step.restype = ctypes.c_int
+    lib.oracle_attention_ragged.argtypes = [_F, _F, _F, _I64, _I32, _F] + [ctypes.c_int] * 5
+    lib.oracle_attention_ragged.restype = ctypes.c_int
+    lib.oracle_prefill.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 8
+    lib.oracle_prefill.restype = ctypes.c_int
+    lib.oracle_max_threads.argtypes = []
+    lib.oracle_max_threads.restype = ctypes.c_int
+    _libs[path] = lib
+    return lib
+
+
+def lib(timing: bool = False) -> ctypes.CDLL:
+    return _load(TIMING_LIB if timing else PARITY_LIB)
+
+
+def _fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- RNG
+def normal(seed: int, shape) -> np.ndarray:
+    """N(0,1) fp32 from stream ``seed`` (splitmix64 -> xoshiro256** -> Box-Muller)."""
+    out = np.empty(shape, dtype=np.float32)
+    lib().tmac_fill_normal(ctypes.c_uint64(seed), _fp(out), out.size)
+    return out
+
+
+def splitmix64(state: int, n: int) -> list[int]:
+    st = ctypes.c_uint64(state)
+    return [lib().tmac_splitmix64(ctypes.byref(st)) for _ in range(n)]
+
+
+# ---------------------------------------------------------------- path
+def rope_heads(x, n_heads: int, head_dim: int, pos: int, base: float = 1e6) -> np.ndarray:
+    y = _f32(x).copy()
+    assert y.size == n_heads * head_dim
+    lib().oracle_rope_heads(_fp(y), n_heads, head_dim, pos, base)
+    return y
+
+
+def rope(q, k, n_head: int, n_kv_head: int, head_dim: int, pos: int, base: float = 1e6):
+    return (rope_heads(q, n_head, head_dim, pos, base), rope_heads(k, n_kv_head, head_dim, pos, base))
+
+
+def rope_theta(head_dim: int, base: float = 1e6) -> np.ndarray:
+    t = np.empty(head_dim // 2, dtype=np.float32)
+    lib().oracle_rope_theta(_fp(t), head_dim, base)
+    return t
+
+
+def cache_write(cache: np.ndarray, row: int, src) -> None:
+    """In place: cache[row, ...] = src (cache is [n_pos][kv_dim] float32)."""
+    src = _f32(src).ravel()
+    dst = cache.reshape(cache.shape[0], -1)
+    assert dst.base is cache or dst is cache or np.shares_memory(dst, cache)
+    view = dst[row]
+    lib().oracle_cache_write(view.ctypes.data_as(_F), _fp(src), src.size)
+
+
+def attention(q, k_cache, v_cache, n_head: int, n_kv_head: int, head_dim: int, past_len: int) -> np.ndarray:
+    q = _f32(q)
+    k_cache = _f32(k_cache)
+    v_cache = _f32(v_cache)
+    assert k_cache.size >= (past_len + 1) * n_kv_head * head_dim
+    out = np.empty(n_head * head_dim, dtype=np.float32)
+    rc = lib().oracle_attention(_fp(q), _fp(k_cache), _fp(v_cache), _fp(out),
+                                n_head, n_kv_head, head_dim, past_len)
+    if rc != 0:
+        raise ValueError("oracle_attention: bad arguments")
+    return out
+
+
+def layer_step(q, k_new, v_new, k_cache: np.ndarray, v_cache: np.ndarray, n_head: int,
+               n_kv_head: int, head_dim: int, pos: int, base: float = 1e6):
+    """Reference decode slice for one layer; updates k_cache/v_cache in place.
+    Returns (out, q_roped, k_roped)."""
+    q = _f32(q).copy()
+    k = _f32(k_new).copy()
+    v = _f32(v_new)
+    assert k_cache.dtype == np.float32 and k_cache.flags["C_CONTIGUOUS"]
+    assert v_cache.dtype == np.float32 and v_cache.flags["C_CONTIGUOUS"]
+    out = np.empty(n_head * head_dim, dtype=np.float32)
+    rc = lib().oracle_layer_step(_fp(q), _fp(k), _fp(v), _fp(k_cache), _fp(v_cache), _fp(out),
+                                 n_head, n_kv_head, head_dim, pos, base)
+    if rc != 0:
+        raise ValueError("oracle_layer_step: bad arguments")
+    return out, q, k
+
+
+def attention_ragged(q, k_pool, v_pool, offsets, lengths, n_head: int, n_kv_head: int,
+                     head_dim: int, n_threads: int = 1, timing: bool = False) -> np.ndarray:
+    q = _f32(q)
+    k_pool = _f32(k_pool)
+    v_pool = _f32(v_pool)
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    lengths = np.ascontiguousarray(lengths, dtype=np.int32)
+    n_seq = lengths.size
+    out = np.empty((n_seq, n_head * head_dim), dtype=np.float32)
+    rc = lib(timing).oracle_attention_ragged(
+        _fp(q), _fp(k_pool), _fp(v_pool), offsets.ctypes.data_as(_I64),
+        lengths.ctypes.data_as(_I32), _fp(out), n_seq, n_head, n_kv_head, head_dim, n_threads)
+    if rc != 0:
+        raise ValueError("oracle_attention_ragged: bad arguments")
+    return out
+
+
+def prefill(q, k_cache, v_cache, n_seq: int, n_q: int, prefix_len: int, seq_capacity: int,
+            n_head: int, n_kv_head: int, head_dim: int, n_threads: int = 1) -> np.ndarray:
+    q = _f32(q)
+    k_cache = _f32(k_cache)
+    v_cache = _f32(v_cache)
+    out = np.empty((n_seq, n_q, n_head * head_dim), dtype=np.float32)
+    rc = lib().oracle_prefill(_fp(q), _fp(k_cache), _fp(v_cache), _fp(out), n_seq, n_q,
+                              prefix_len, seq_capacity, n_head, n_kv_head, head_dim, n_threads)
+    if rc != 0:
+        raise ValueError("oracle_prefill: bad arguments")
+    return out
+
+
+def max_threads(timing: bool = False) -> int:
+    return lib(timing).oracle_max_threads()

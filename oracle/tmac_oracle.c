@@ -1,0 +1,282 @@
+/*
+ * tmac_oracle.c -- CPU restatement of the reference's attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker and CPU baseline for
+ * libtmac_attn.so.  Nothing in the product links or calls it.
+ *
+ * Each function cites the reference lines it follows (liuwantao3/tmac_gguf.cpp).
+ * Parity build: gcc -O2 -ffp-contract=off (no fused multiply-add, glibc libm).
+ */
+#include "tmac_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* RNG.  splitmix64 (Steele, Lea, Flood 2014) seeds xoshiro256** (Blackman,  */
+/* Vigna 2018); normals by the Box-Muller transform in double, cast to fp32. */
+/* ------------------------------------------------------------------------ */
+uint64_t tmac_splitmix64(uint64_t* state) {
+    uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static inline uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+
+void tmac_rng_seed(tmac_rng* r, uint64_t seed) {
+    uint64_t st = seed;
+    for (int i = 0; i < 4; i++) r->s[i] = tmac_splitmix64(&st);
+    r->has_spare = 0;
+    r->spare = 0.0;
+}
+
+uint64_t tmac_rng_next(tmac_rng* r) {
+    uint64_t* s = r->s;
+    const uint64_t result = rotl64(s[1] * 5, 7) * 9;
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = rotl64(s[3], 45);
+    return result;
+}
+
+double tmac_rng_uniform(tmac_rng* r) { return (double)(tmac_rng_next(r) >> 11) * 0x1.0p-53; }
+
+void tmac_rng_normal_f32(tmac_rng* r, float* out, size_t n) {
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i++) {
+        if (r->has_spare) {
+            r->has_spare = 0;
+            out[i] = (float)r->spare;
+            continue;
+        }
+        double u1 = 1.0 - tmac_rng_uniform(r); /* (0, 1] so log() is finite */
+        double u2 = tmac_rng_uniform(r);
+        double rad = sqrt(-2.0 * log(u1));
+        double a = two_pi * u2;
+        r->spare = rad * sin(a);
+        r->has_spare = 1;
+        out[i] = (float)(rad * cos(a));
+    }
+}
+
+void tmac_fill_normal(uint64_t seed, float* out, size_t n) {
+    tmac_rng r;
+    tmac_rng_seed(&r, seed);
+    tmac_rng_normal_f32(&r, out, n);
+}
+
+/* ------------------------------------------------------------------------ */
+/* RoPE -- tmac_gguf.cpp:990-1016.  GPT-J style: adjacent pairs (d, d+1),    */
+/* theta = 1/powf(base, d/head_dim) for even d, angle = pos*theta in fp32.   */
+/* ------------------------------------------------------------------------ */
+void oracle_rope_heads(float* x, int n_heads, int head_dim, int pos, float base) {
+    for (int h = 0; h < n_heads; h++) {                                /* :992 / :1004 */
+        for (int d = 0; d < head_dim; d += 2) {                        /* :993 / :1005 */
+            float theta = 1.0f / powf(base, (float)d / head_dim);      /* :994 */
+            float freq = pos * theta;                                  /* :995 */
+            float cos_val = cosf(freq);                                /* :996 */
+            float sin_val = sinf(freq);                                /* :997 */
+            int idx = h * head_dim + d;                                /* :998 */
+            float x0 = x[idx], x1 = x[idx + 1];                        /* :999 */
+            x[idx] = x0 * cos_val - x1 * sin_val;                      /* :1000 */
+            x[idx + 1] = x0 * sin_val + x1 * cos_val;                  /* :1001 */
+        }
+    }
+}
+
+void oracle_rope(float* q, float* k, int n_head, int n_kv_head, int head_dim, int pos, float base) {
+    oracle_rope_heads(q, n_head, head_dim, pos, base);    /* :992-1003 */
+    oracle_rope_heads(k, n_kv_head, head_dim, pos, base); /* :1004-1015 */
+}
+
+void oracle_rope_theta(float* theta, int head_dim, float base) {
+    for (int d = 0; d < head_dim; d += 2) theta[d / 2] = 1.0f / powf(base, (float)d / head_dim);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Cache write -- tmac_gguf.cpp:1090-1091.                                   */
+/* ------------------------------------------------------------------------ */
+void oracle_cache_write(float* cache_row, const float* src, int dim) {
+    for (int i = 0; i < dim; i++) cache_row[i] = src[i];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Attention -- tmac_gguf.cpp:1093-1128, one query head.                    */
+/* `scores` has room for past_len+1 floats.                                  */
+/* ------------------------------------------------------------------------ */
+static void attention_head(const float* qh_data, const float* k_cache, const float* v_cache,
+                           float* ctx_h, float* scores, int kv, int n_kv_head, int head_dim,
+                           int past_len) {
+    const int pos = past_len;
+    const size_t row = (size_t)n_kv_head * head_dim; /* K_DIM: one cache row per position */
+
+    for (int d = 0; d < head_dim; d++) ctx_h[d] = 0.0f;                       /* :1094 memset */
+    for (int p = 0; p <= pos; p++) scores[p] = 0;                             /* :1104 */
+    for (int d = 0; d < head_dim; d++) {                                      /* :1105 */
+        float q_val = qh_data[d];                                             /* :1106 */
+        for (int p = 0; p <= pos; p++) {                                      /* :1107 */
+            const float* k_cached = k_cache + (size_t)p * row + (size_t)kv * head_dim; /* :1108 */
+            scores[p] += q_val * k_cached[d];                                 /* :1109 */
+        }
+    }
+    for (int p = 0; p <= pos; p++) scores[p] /= sqrtf((float)head_dim);      /* :1112 */
+
+    float max_score = scores[0];                                              /* :1114 */
+    for (int p = 1; p <= pos; p++)
+        if (scores[p] > max_score) max_score = scores[p];                     /* :1115 */
+    float exp_sum = 0;                                                        /* :1116 */
+    for (int p = 0; p <= pos; p++) exp_sum += expf(scores[p] - max_score);    /* :1117 */
+    float log_sum = logf(exp_sum) + max_score;                                /* :1118 */
+
+    for (int p = 0; p <= pos; p++) {                                          /* :1120 */
+        const float* v_cached = v_cache + (size_t)p * row + (size_t)kv * head_dim; /* :1121 */
+        float exp_score = expf(scores[p] - log_sum);                          /* :1122 */
+        for (int d = 0; d < head_dim; d++) ctx_h[d] += exp_score * v_cached[d]; /* :1123-1124 */
+    }
+}
+
+static int bad_shape(int n_head, int n_kv_head, int head_dim, int past_len) {
+    return n_head <= 0 || n_kv_head <= 0 || head_dim <= 0 || past_len < 0 ||
+           (n_head % n_kv_head) != 0;
+}
+
+int oracle_attention(const float* q, const float* k_cache, const float* v_cache, float* out,
+                     int n_head, int n_kv_head, int head_dim, int past_len) {
+    if (bad_shape(n_head, n_kv_head, head_dim, past_len)) return -1;
+    float* scores = (float*)malloc(sizeof(float) * ((size_t)past_len + 1));
+    if (!scores) return -1;
+    int q_per_kv = n_head / n_kv_head;                                        /* :1096 */
+    for (int qh = 0; qh < n_head; qh++) {                                     /* :1098 */
+        int kv = qh / q_per_kv;                                               /* :1099 */
+        attention_head(q + (size_t)qh * head_dim, k_cache, v_cache, out + (size_t)qh * head_dim,
+                       scores, kv, n_kv_head, head_dim, past_len);
+    }
+    free(scores);
+    return 0;
+}
+
+int oracle_layer_step(float* q, float* k_new, const float* v_new,
+                      float* k_cache_layer, float* v_cache_layer, float* out,
+                      int n_head, int n_kv_head, int head_dim, int pos, float base) {
+    if (bad_shape(n_head, n_kv_head, head_dim, pos)) return -1;
+    const int kdim = n_kv_head * head_dim;
+    oracle_rope(q, k_new, n_head, n_kv_head, head_dim, pos, base);               /* :1085-1088 */
+    oracle_cache_write(k_cache_layer + (size_t)pos * kdim, k_new, kdim);         /* :1090 */
+    oracle_cache_write(v_cache_layer + (size_t)pos * kdim, v_new, kdim);         /* :1091 */
+    return oracle_attention(q, k_cache_layer, v_cache_layer, out,                /* :1093-1128 */
+                            n_head, n_kv_head, head_dim, pos);
+}
+
+int oracle_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* Runs the per-head computation for every (unit, head); `units` rows each name
+ * a q row, a cache base and a past_len. */
+typedef struct {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* out;
+    int past_len;
+} unit_desc;
+
+static int run_units(const unit_desc* units, long n_units, int n_head, int n_kv_head,
+                     int head_dim, int n_threads) {
+    int max_past = 0;
+    for (long u = 0; u < n_units; u++) {
+        if (bad_shape(n_head, n_kv_head, head_dim, units[u].past_len)) return -1;
+        if (units[u].past_len > max_past) max_past = units[u].past_len;
+    }
+    const int q_per_kv = n_head / n_kv_head;
+    const long n_work = n_units * n_head;
+    int rc = 0;
+#ifdef _OPENMP
+    if (n_threads < 1) n_threads = 1;
+#pragma omp parallel num_threads(n_threads)
+#endif
+    {
+        float* scores = (float*)malloc(sizeof(float) * ((size_t)max_past + 1));
+        if (!scores) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+            rc = -1;
+        } else {
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+            for (long w = 0; w < n_work; w++) {
+                const unit_desc* ud = &units[w / n_head];
+                int qh = (int)(w % n_head);
+                attention_head(ud->q + (size_t)qh * head_dim, ud->k, ud->v,
+                               ud->out + (size_t)qh * head_dim, scores, qh / q_per_kv,
+                               n_kv_head, head_dim, ud->past_len);
+            }
+            free(scores);
+        }
+    }
+    (void)n_threads;
+    return rc;
+}
+
+int oracle_attention_ragged(const float* q, const float* k_pool, const float* v_pool,
+                            const int64_t* offsets, const int32_t* lengths, float* out,
+                            int n_seq, int n_head, int n_kv_head, int head_dim, int n_threads) {
+    if (n_seq < 0) return -1;
+    if (n_seq == 0) return 0;
+    unit_desc* units = (unit_desc*)malloc(sizeof(unit_desc) * (size_t)n_seq);
+    if (!units) return -1;
+    const size_t row = (size_t)n_kv_head * head_dim;
+    const size_t qsz = (size_t)n_head * head_dim;
+    for (int s = 0; s < n_seq; s++) {
+        if (lengths[s] < 1 || offsets[s] < 0) { free(units); return -1; }
+        units[s].q = q + (size_t)s * qsz;
+        units[s].k = k_pool + (size_t)offsets[s] * row;
+        units[s].v = v_pool + (size_t)offsets[s] * row;
+        units[s].out = out + (size_t)s * qsz;
+        units[s].past_len = lengths[s] - 1;
+    }
+    int rc = run_units(units, n_seq, n_head, n_kv_head, head_dim, n_threads);
+    free(units);
+    return rc;
+}
+
+int oracle_prefill(const float* q, const float* k_cache, const float* v_cache, float* out,
+                   int n_seq, int n_q, int prefix_len, int seq_capacity,
+                   int n_head, int n_kv_head, int head_dim, int n_threads) {
+    if (n_seq < 0 || n_q < 0 || prefix_len < 0 || prefix_len + n_q > seq_capacity) return -1;
+    long n_units = (long)n_seq * n_q;
+    if (n_units == 0) return 0;
+    unit_desc* units = (unit_desc*)malloc(sizeof(unit_desc) * (size_t)n_units);
+    if (!units) return -1;
+    const size_t row = (size_t)n_kv_head * head_dim;
+    const size_t qsz = (size_t)n_head * head_dim;
+    for (int s = 0; s < n_seq; s++) {
+        for (int i = 0; i < n_q; i++) {
+            unit_desc* ud = &units[(long)s * n_q + i];
+            ud->q = q + ((size_t)s * n_q + i) * qsz;
+            ud->out = out + ((size_t)s * n_q + i) * qsz;
+            ud->k = k_cache + (size_t)s * seq_capacity * row;
+            ud->v = v_cache + (size_t)s * seq_capacity * row;
+            ud->past_len = prefix_len + i;
+        }
+    }
+    int rc = run_units(units, n_units, n_head, n_kv_head, head_dim, n_threads);
+    free(units);
+    return rc;
+}

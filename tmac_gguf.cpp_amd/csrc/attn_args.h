@@ -1,0 +1,65 @@
+// attn_args.h -- kernel argument blocks shared by the host layer (tmac_attn.cpp)
+// and the gfx950 kernels (attn_kernels.hip).  Every kernel takes one of these
+// structs by value as its only argument, so hipModuleLaunchKernel passes a
+// single pointer in kernelParams.
+#pragma once
+#include <stdint.h>
+
+namespace tmac {
+
+constexpr int kHeadDim = 64;        // the reference's flash kernel supports only 64 (kernel_flash_attn.metal:18)
+constexpr int kSlotsPerWave = 16;   // 64 lanes = 16 (position, kv-head) slots x 4 dim-lanes
+constexpr int kWavesPerGroup = 4;   // workgroup = 256 threads
+constexpr int kPartialStride = kHeadDim + 2;  // per (split, head): acc[64], m, l
+
+// Attention over a KV cache in the reference layout: one row per position,
+// row = [n_kv_head][64] fp32 (tmac_gguf.cpp:200-201).
+struct DecodeArgs {
+    const float* q;          // [n_seq][n_head][64]; layer mode: pre-RoPE q of one token
+    const float* k;          // cache / pool base
+    const float* v;
+    float* out;              // [n_seq][n_head][64]
+    const int64_t* offsets;  // ragged mode: first row of each sequence in the pool
+    const int32_t* lengths;  // ragged mode: rows per sequence
+    int64_t seq_stride;      // uniform mode: rows between consecutive sequences
+    int n_pos;               // uniform mode: rows attended per sequence (past_len + 1)
+    int n_head;
+    int split_len;           // rows per workgroup (multiple of the group's step)
+    int n_splits;            // gridDim.x
+    float* ws;               // split partials [n_seq][n_splits][n_head][66] (n_splits > 1)
+    int* counters;           // [n_seq] arrival counters, zero between launches
+    float qscale;            // log2(e) / sqrt(head_dim): softmax runs in base 2
+    // layer mode (RoPE + cache write + attention in one launch)
+    const float* k_new;      // [n_kv_head][64] pre-RoPE
+    const float* v_new;      // [n_kv_head][64]
+    const float2* rope_cs;   // [rope_rows][32] (cos, sin) of pos*theta_j
+    const int* pos_dev;      // device-side position (graph replay); null -> pos_host
+    int pos_host;
+    int rope_rows;
+    int capacity;            // rows in the layer cache
+    int* err;                // device error word (bit 0: position out of range)
+};
+
+struct RopeArgs {
+    float* x;                // [n_heads][64], rotated in place
+    const float2* rope_cs;   // [rope_rows][32]
+    const int* pos_dev;
+    int pos_host;
+    int n_heads;
+    int rope_rows;
+    int* err;
+};
+
+struct CopyArgs {
+    float* dst;
+    const float* src;
+    int n;
+};
+
+struct PosArgs {
+    int* pos;
+    int value;
+    int add;                 // 0: *pos = value; 1: *pos += value
+};
+
+}  // namespace tmac

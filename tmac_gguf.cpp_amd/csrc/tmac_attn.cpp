@@ -1,0 +1,759 @@
+// tmac_attn.cpp -- host layer of libtmac_attn.so: the C ABI declared in
+// include/tmac_attn.h, implemented over the HIP runtime.
+//
+// Replaces the reference's Metal backend for the attention path:
+//   init / shutdown              metal_backend.cpp:21-89, metal_backend.hpp:519-520
+//   attention_op / rope_op / elem_op   metal_backend.hpp:354-453
+//   metal_batch_begin / _end     metal_backend.hpp:114-122, 176-190 (-> hipGraph capture)
+// The gfx950 code object (attn_kernels.hip) is linked into this library as
+// bytes and loaded with hipModuleLoadData; kernels launch with
+// hipModuleLaunchKernel.  There is no CPU fallback: without a gfx950 device
+// tmac_init fails and every other entry point reports TMAC_ERR_NOT_INITIALIZED.
+#include "tmac_attn.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "attn_args.h"
+
+extern "C" const unsigned char tmac_attn_code_object[];
+extern "C" const uint64_t tmac_attn_code_object_size;
+
+using tmac::CopyArgs;
+using tmac::DecodeArgs;
+using tmac::PosArgs;
+using tmac::RopeArgs;
+using tmac::kHeadDim;
+using tmac::kPartialStride;
+using tmac::kSlotsPerWave;
+using tmac::kWavesPerGroup;
+
+namespace {
+
+constexpr int kBlock = kWavesPerGroup * 64;
+// (G = n_head / n_kv_head, KV = n_kv_head) pairs compiled into the code object.
+constexpr int kShapes[][2] = {{7, 2}, {1, 1}, {1, 2}, {2, 2}, {4, 2}, {4, 4}, {8, 1}};
+enum { kModeUniform = 0, kModeRagged = 1, kModeLayer = 2 };
+
+struct RopeTable {
+    int head_dim;
+    uint32_t base_bits;
+    float2* dev;
+    int rows;
+};
+
+}  // namespace
+
+struct tmac_graph {
+    hipGraphExec_t exec = nullptr;
+};
+
+struct tmac_context {
+    int device = -1;
+    int n_cu = 0;
+    hipModule_t module = nullptr;
+    std::map<std::pair<int, int>, hipFunction_t> decode[3];  // by mode, (G, KV)
+    hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr;
+    float* ws = nullptr;
+    size_t ws_floats = 0;
+    int* counters = nullptr;
+    int n_counters = 0;
+    int* err = nullptr;
+    std::vector<RopeTable> rope;
+    int64_t opt_split_len = 0;
+    int64_t opt_target_groups = 0;
+    std::string last_error;
+    char device_name[256] = {0};
+};
+
+namespace {
+
+int fail(tmac_context* ctx, int code, const std::string& msg) {
+    if (ctx) ctx->last_error = msg;
+    return code;
+}
+
+int hip_fail(tmac_context* ctx, hipError_t e, const char* what) {
+    if (ctx) ctx->last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return TMAC_ERR_HIP_BASE + (int)e;
+}
+
+#define HIP_TRY(ctx, expr)                                   \
+    do {                                                     \
+        hipError_t e_ = (expr);                              \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, #expr); \
+    } while (0)
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_ctx(tmac_context* ctx) {
+    if (!ctx || !ctx->module) return TMAC_ERR_NOT_INITIALIZED;
+    return TMAC_OK;
+}
+
+int set_device(tmac_context* ctx) {
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    return TMAC_OK;
+}
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
+    return st != hipStreamCaptureStatusNone;
+}
+
+// Validates the attention shape shared by every decode entry point.
+int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, hipFunction_t* fn_out,
+                int mode) {
+    if (head_dim != kHeadDim)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "head_dim must be 64 (got " + std::to_string(head_dim) + ")");
+    if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head != 0)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "n_head must be a positive multiple of n_kv_head");
+    const int g = n_head / n_kv_head;
+    auto it = ctx->decode[mode].find({g, n_kv_head});
+    if (it == ctx->decode[mode].end())
+        return fail(ctx, TMAC_ERR_UNSUPPORTED,
+                    "no kernel for n_head/n_kv_head = " + std::to_string(g) + ", n_kv_head = " +
+                        std::to_string(n_kv_head));
+    *fn_out = it->second;
+    return TMAC_OK;
+}
+
+// Rows per workgroup: a multiple of one round of steps over the workgroup
+// (kWavesPerGroup steps of 16/n_kv_head rows); aims for `target` workgroups
+// (2 per CU by default) without going below one round per workgroup.
+void choose_split(const tmac_context* ctx, int n_seq, int n_pos, int n_kv_head, int* split_len, int* n_splits) {
+    const int round = kWavesPerGroup * (kSlotsPerWave / n_kv_head);
+    const int rounds = (n_pos + round - 1) / round;
+    int len;
+    if (ctx->opt_split_len > 0) {
+        len = (int)(((ctx->opt_split_len + round - 1) / round) * round);
+    } else {
+        const int64_t target = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : 2LL * ctx->n_cu;
+        int64_t want = (target + n_seq - 1) / (n_seq > 0 ? n_seq : 1);
+        if (want < 1) want = 1;
+        if (want > rounds) want = rounds;
+        const int64_t per = (rounds + want - 1) / want;
+        len = (int)(per * round);
+    }
+    if (len < round) len = round;
+    *split_len = len;
+    *n_splits = (n_pos + len - 1) / len;
+    if (*n_splits < 1) *n_splits = 1;
+}
+
+int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats, int counters) {
+    if (floats <= ctx->ws_floats && counters <= ctx->n_counters) return TMAC_OK;
+    if (capturing(stream))
+        return fail(ctx, TMAC_ERR_CAPTURE,
+                    "split-KV workspace must grow but the stream is capturing; run the same shape once "
+                    "before capture");
+    HIP_TRY(ctx, hipDeviceSynchronize());
+    if (floats > ctx->ws_floats) {
+        size_t n = ctx->ws_floats ? ctx->ws_floats : (1u << 20);
+        while (n < floats) n *= 2;
+        float* p = nullptr;
+        HIP_TRY(ctx, hipMalloc(&p, n * sizeof(float)));
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        ctx->ws = p;
+        ctx->ws_floats = n;
+    }
+    if (counters > ctx->n_counters) {
+        int n = ctx->n_counters ? ctx->n_counters : 1024;
+        while (n < counters) n *= 2;
+        int* p = nullptr;
+        HIP_TRY(ctx, hipMalloc(&p, (size_t)n * sizeof(int)));
+        HIP_TRY(ctx, hipMemset(p, 0, (size_t)n * sizeof(int)));
+        HIP_TRY(ctx, hipDeviceSynchronize());
+        if (ctx->counters) (void)hipFree(ctx->counters);
+        ctx->counters = p;
+        ctx->n_counters = n;
+    }
+    return TMAC_OK;
+}
+
+uint32_t float_bits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+
+// cos/sin of pos*theta_j exactly as tmac_gguf.cpp:994-997 computes them
+// (fp32 theta = 1/powf(base, d/head_dim), fp32 angle = pos*theta, libm
+// cosf/sinf); built on the host so the device rotation is bit-identical to
+// the reference's CPU path.  This file is compiled with -ffp-contract=off
+// -fno-builtin so that nothing is fused or merged into sincosf.
+int rope_table(tmac_context* ctx, hipStream_t stream, int head_dim, float base, int need_rows,
+               const RopeTable** out) {
+    RopeTable* found = nullptr;
+    for (auto& t : ctx->rope)
+        if (t.head_dim == head_dim && t.base_bits == float_bits(base)) found = &t;
+    if (found && found->rows >= need_rows) {
+        *out = found;
+        return TMAC_OK;
+    }
+    if (capturing(stream))
+        return fail(ctx, TMAC_ERR_CAPTURE,
+                    "RoPE table must grow but the stream is capturing; call tmac_rope_prepare first");
+    int rows = found ? found->rows : 0;
+    int new_rows = rows > 0 ? rows : 4096;
+    while (new_rows < need_rows) {
+        if (new_rows > INT_MAX / 2) { new_rows = need_rows; break; }
+        new_rows *= 2;
+    }
+    const int pairs = head_dim / 2;
+    std::vector<float2> host((size_t)new_rows * pairs);
+    for (int pos = 0; pos < new_rows; pos++) {
+        for (int d = 0; d < head_dim; d += 2) {
+            float theta = 1.0f / powf(base, (float)d / head_dim);
+            float freq = pos * theta;
+            host[(size_t)pos * pairs + d / 2] = make_float2(cosf(freq), sinf(freq));
+        }
+    }
+    float2* dev = nullptr;
+    HIP_TRY(ctx, hipDeviceSynchronize());
+    HIP_TRY(ctx, hipMalloc(&dev, host.size() * sizeof(float2)));
+    HIP_TRY(ctx, hipMemcpy(dev, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice));
+    if (found) {
+        (void)hipFree(found->dev);
+        found->dev = dev;
+        found->rows = new_rows;
+    } else {
+        ctx->rope.push_back(RopeTable{head_dim, float_bits(base), dev, new_rows});
+        found = &ctx->rope.back();
+    }
+    *out = found;
+    return TMAC_OK;
+}
+
+int launch(tmac_context* ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned block, hipStream_t stream,
+           void* args) {
+    void* params[] = {args};
+    HIP_TRY(ctx, hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, 0, stream, params, nullptr));
+    return TMAC_OK;
+}
+
+const float kQScale = (float)(1.4426950408889634 / 8.0);  // log2(e) / sqrt(64)
+
+// Common launch of a decode-family kernel.
+int run_decode(tmac_context* ctx, hipStream_t stream, hipFunction_t fn, DecodeArgs& a, int n_seq,
+               int grid_rows, int n_kv_head) {
+    int split_len = 0, n_splits = 0;
+    choose_split(ctx, n_seq, grid_rows, n_kv_head, &split_len, &n_splits);
+    a.split_len = split_len;
+    a.n_splits = n_splits;
+    a.qscale = kQScale;
+    a.err = ctx->err;
+    if (n_splits > 1) {
+        const size_t need = (size_t)n_seq * n_splits * a.n_head * kPartialStride;
+        int rc = ensure_workspace(ctx, stream, need, n_seq);
+        if (rc) return rc;
+        a.ws = ctx->ws;
+        a.counters = ctx->counters;
+    } else {
+        a.ws = nullptr;
+        a.counters = nullptr;
+    }
+    if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
+    return launch(ctx, fn, (unsigned)n_splits, (unsigned)n_seq, kBlock, stream, &a);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tmac_status_string(int status) {
+    switch (status) {
+        case TMAC_OK: return "ok";
+        case TMAC_ERR_INVALID_ARG: return "invalid argument";
+        case TMAC_ERR_NULL_POINTER: return "null pointer";
+        case TMAC_ERR_MISALIGNED: return "pointer not 16-byte aligned";
+        case TMAC_ERR_UNSUPPORTED: return "unsupported shape or operation";
+        case TMAC_ERR_CAPACITY: return "position or size beyond capacity";
+        case TMAC_ERR_NOT_INITIALIZED: return "context not initialized";
+        case TMAC_ERR_CAPTURE: return "not allowed while the stream is capturing";
+        case TMAC_ERR_DEVICE_FAULT: return "device reported an out-of-range position";
+        default: break;
+    }
+    if (status >= TMAC_ERR_HIP_BASE) return hipGetErrorString((hipError_t)(status - TMAC_ERR_HIP_BASE));
+    return "unknown status";
+}
+
+const char* tmac_last_error(const tmac_context* ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+int tmac_abi_version(void) { return TMAC_ATTN_ABI_VERSION; }
+
+int tmac_init(tmac_context** out, int device) {
+    if (!out) return TMAC_ERR_NULL_POINTER;
+    *out = nullptr;
+    auto* ctx = new tmac_context();
+    ctx->device = device;
+    int n_dev = 0;
+    hipError_t e = hipGetDeviceCount(&n_dev);
+    if (e != hipSuccess || n_dev <= device || device < 0) {
+        int rc = e != hipSuccess ? hip_fail(ctx, e, "hipGetDeviceCount")
+                                 : fail(ctx, TMAC_ERR_INVALID_ARG, "no such device");
+        delete ctx;
+        return rc;
+    }
+    auto bail = [&](int rc) {
+        if (ctx->module) (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return rc;
+    };
+    if ((e = hipSetDevice(device)) != hipSuccess) return bail(hip_fail(ctx, e, "hipSetDevice"));
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
+        return bail(hip_fail(ctx, e, "hipGetDeviceProperties"));
+    ctx->n_cu = prop.multiProcessorCount;
+    std::snprintf(ctx->device_name, sizeof(ctx->device_name), "%s", prop.gcnArchName);
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        fprintf(stderr, "[tmac] device %d is %s; this library is built for gfx950 only\n", device,
+                prop.gcnArchName);
+        return bail(TMAC_ERR_UNSUPPORTED);
+    }
+    if ((e = hipModuleLoadData(&ctx->module, tmac_attn_code_object)) != hipSuccess)
+        return bail(hip_fail(ctx, e, "hipModuleLoadData"));
+    const char* mode_prefix[3] = {"tmac_decode_u", "tmac_decode_r", "tmac_layer"};
+    for (int m = 0; m < 3; m++) {
+        for (auto& sh : kShapes) {
+            char name[64];
+            std::snprintf(name, sizeof(name), "%s_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
+            hipFunction_t f = nullptr;
+            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                return bail(hip_fail(ctx, e, name));
+            ctx->decode[m][{sh[0], sh[1]}] = f;
+        }
+    }
+    if ((e = hipModuleGetFunction(&ctx->k_rope, ctx->module, "tmac_rope")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->k_copy, ctx->module, "tmac_copy")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->k_pos, ctx->module, "tmac_pos_update")) != hipSuccess)
+        return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
+    if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
+    if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
+    int rc = ensure_workspace(ctx, nullptr, (size_t)1 << 20, 1024);
+    if (rc) return bail(rc);
+    *out = ctx;
+    return TMAC_OK;
+}
+
+int tmac_shutdown(tmac_context* ctx) {
+    if (!ctx) return TMAC_ERR_NOT_INITIALIZED;
+    if (ctx->module) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipDeviceSynchronize();
+        for (auto& t : ctx->rope) (void)hipFree(t.dev);
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        if (ctx->counters) (void)hipFree(ctx->counters);
+        if (ctx->err) (void)hipFree(ctx->err);
+        (void)hipModuleUnload(ctx->module);
+    }
+    delete ctx;
+    return TMAC_OK;
+}
+
+int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
+                      const float* v_cache, float* out, int n_head, int n_kv_head, int head_dim,
+                      int past_len) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !k_cache || !v_cache || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "attention_op: null buffer");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "attention_op: buffers must be 16-byte aligned");
+    hipFunction_t fn;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeUniform))) return rc;
+    if (past_len < 0 || past_len == INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "past_len out of range");
+    if ((rc = set_device(ctx))) return rc;
+    DecodeArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.out = out;
+    a.seq_stride = 0;
+    a.n_pos = past_len + 1;
+    a.n_head = n_head;
+    return run_decode(ctx, (hipStream_t)stream, fn, a, 1, past_len + 1, n_kv_head);
+}
+
+int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const float* q, const float* k,
+                                  const float* v, float* out, int n_seq, int n_head, int n_kv_head,
+                                  int head_dim, int n_pos, int64_t seq_stride) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !k || !v || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "decode_batched: null buffer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "decode_batched: buffers must be 16-byte aligned");
+    hipFunction_t fn;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeUniform))) return rc;
+    if (n_seq < 0 || n_pos < 1 || seq_stride < 0 || (n_seq > 1 && seq_stride < n_pos))
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_batched: need n_seq >= 0, n_pos >= 1, seq_stride >= n_pos");
+    if (n_seq == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    DecodeArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.seq_stride = seq_stride;
+    a.n_pos = n_pos;
+    a.n_head = n_head;
+    return run_decode(ctx, (hipStream_t)stream, fn, a, n_seq, n_pos, n_kv_head);
+}
+
+int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const float* q,
+                                 const float* k_pool, const float* v_pool, const int64_t* offsets,
+                                 const int32_t* lengths, float* out, int n_seq, int n_head,
+                                 int n_kv_head, int head_dim, int max_len) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !k_pool || !v_pool || !offsets || !lengths || !out)
+        return fail(ctx, TMAC_ERR_NULL_POINTER, "decode_ragged: null buffer");
+    if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "decode_ragged: buffers must be 16-byte aligned");
+    hipFunction_t fn;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeRagged))) return rc;
+    if (n_seq < 0 || max_len < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: need max_len >= 1");
+    if (n_seq == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    DecodeArgs a{};
+    a.q = q;
+    a.k = k_pool;
+    a.v = v_pool;
+    a.out = out;
+    a.offsets = offsets;
+    a.lengths = lengths;
+    a.n_head = n_head;
+    return run_decode(ctx, (hipStream_t)stream, fn, a, n_seq, max_len, n_kv_head);
+}
+
+static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, const float* k_new,
+                        const float* v_new, float* k_cache, float* v_cache, float* out, int n_head,
+                        int n_kv_head, int head_dim, int pos, const int* pos_dev, int capacity,
+                        float base) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !k_new || !v_new || !k_cache || !v_cache || !out)
+        return fail(ctx, TMAC_ERR_NULL_POINTER, "layer_attention: null buffer");
+    if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new) || !aligned16(k_cache) ||
+        !aligned16(v_cache) || !aligned16(out))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "layer_attention: buffers must be 16-byte aligned");
+    hipFunction_t fn;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeLayer))) return rc;
+    if (capacity < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "layer_attention: capacity < 1");
+    if (!pos_dev && (pos < 0 || pos >= capacity))
+        return fail(ctx, TMAC_ERR_CAPACITY, "layer_attention: pos outside [0, capacity)");
+    if (!(base > 0.f) || !std::isfinite(base)) return fail(ctx, TMAC_ERR_INVALID_ARG, "layer_attention: bad base");
+    if ((rc = set_device(ctx))) return rc;
+    const RopeTable* rt = nullptr;
+    if ((rc = rope_table(ctx, stream, head_dim, base, pos_dev ? capacity : pos + 1, &rt))) return rc;
+    DecodeArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.out = out;
+    a.n_head = n_head;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.rope_cs = rt->dev;
+    a.rope_rows = rt->rows;
+    a.pos_dev = pos_dev;
+    a.pos_host = pos;
+    a.capacity = capacity;
+    return run_decode(ctx, stream, fn, a, 1, pos_dev ? capacity : pos + 1, n_kv_head);
+}
+
+int tmac_layer_attention(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_new,
+                         const float* v_new, float* k_cache, float* v_cache, float* out, int n_head,
+                         int n_kv_head, int head_dim, int pos, int capacity, float base) {
+    return layer_common(ctx, (hipStream_t)stream, q, k_new, v_new, k_cache, v_cache, out, n_head,
+                        n_kv_head, head_dim, pos, nullptr, capacity, base);
+}
+
+int tmac_layer_attention_devpos(tmac_context* ctx, tmac_stream stream, const float* q,
+                                const float* k_new, const float* v_new, float* k_cache,
+                                float* v_cache, float* out, int n_head, int n_kv_head, int head_dim,
+                                const int* pos_dev, int capacity, float base) {
+    if (!pos_dev) return fail(ctx, TMAC_ERR_NULL_POINTER, "layer_attention_devpos: null pos_dev");
+    return layer_common(ctx, (hipStream_t)stream, q, k_new, v_new, k_cache, v_cache, out, n_head,
+                        n_kv_head, head_dim, 0, pos_dev, capacity, base);
+}
+
+int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!pos_dev) return fail(ctx, TMAC_ERR_NULL_POINTER, "pos_update: null pointer");
+    if ((rc = set_device(ctx))) return rc;
+    PosArgs a{pos_dev, value, add ? 1 : 0};
+    return launch(ctx, ctx->k_pos, 1, 1, 64, (hipStream_t)stream, &a);
+}
+
+int tmac_rope_prepare(tmac_context* ctx, int head_dim, float base, int n_pos) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope: head_dim must be 64");
+    if (n_pos < 1 || !(base > 0.f) || !std::isfinite(base))
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_prepare: need n_pos >= 1 and base > 0");
+    if ((rc = set_device(ctx))) return rc;
+    const RopeTable* rt;
+    return rope_table(ctx, nullptr, head_dim, base, n_pos, &rt);
+}
+
+int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads, int head_dim, int pos,
+                 float base) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!data) return fail(ctx, TMAC_ERR_NULL_POINTER, "rope_op: null data");
+    if (!aligned16(data)) return fail(ctx, TMAC_ERR_MISALIGNED, "rope_op: data must be 16-byte aligned");
+    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope_op: head_dim must be 64");
+    if (n_heads < 0 || pos < 0 || pos == INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_op: bad n_heads/pos");
+    if (!(base > 0.f) || !std::isfinite(base)) return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_op: bad base");
+    if (n_heads == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    const RopeTable* rt = nullptr;
+    if ((rc = rope_table(ctx, (hipStream_t)stream, head_dim, base, pos + 1, &rt))) return rc;
+    RopeArgs a{data, rt->dev, nullptr, pos, n_heads, rt->rows, ctx->err};
+    const int threads = n_heads * (kHeadDim / 2);
+    return launch(ctx, ctx->k_rope, (unsigned)((threads + 255) / 256), 1, 256, (hipStream_t)stream, &a);
+}
+
+int tmac_elem_op(tmac_context* ctx, tmac_stream stream, int op, float* data, const float* aux, int dim) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (op != 2)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "elem_op: only op 2 (cache write) is on the attention path");
+    if (!data || !aux) return fail(ctx, TMAC_ERR_NULL_POINTER, "elem_op: null buffer");
+    if (dim < 0) return fail(ctx, TMAC_ERR_INVALID_ARG, "elem_op: dim < 0");
+    if (dim == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    CopyArgs a{data, aux, dim};
+    return launch(ctx, ctx->k_copy, (unsigned)((dim + 255) / 256), 1, 256, (hipStream_t)stream, &a);
+}
+
+int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (value < 0) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: negative value");
+    switch (option) {
+        case TMAC_OPT_SPLIT_LEN: ctx->opt_split_len = value; return TMAC_OK;
+        case TMAC_OPT_TARGET_GROUPS: ctx->opt_target_groups = value; return TMAC_OK;
+        default: return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: unknown option");
+    }
+}
+
+int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_kv_head, int* split_len,
+                     int* n_splits) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!split_len || !n_splits) return TMAC_ERR_NULL_POINTER;
+    hipFunction_t fn;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, kHeadDim, &fn, kModeUniform))) return rc;
+    if (n_seq < 1 || n_pos < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "query_split: n_seq, n_pos >= 1");
+    choose_split(ctx, n_seq, n_pos, n_kv_head, split_len, n_splits);
+    return TMAC_OK;
+}
+
+int tmac_check_device_error(tmac_context* ctx) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(ctx, hipDeviceSynchronize());
+    int v = 0;
+    HIP_TRY(ctx, hipMemcpy(&v, ctx->err, sizeof(int), hipMemcpyDeviceToHost));
+    if (v) {
+        HIP_TRY(ctx, hipMemset(ctx->err, 0, sizeof(int)));
+        HIP_TRY(ctx, hipDeviceSynchronize());
+        return fail(ctx, TMAC_ERR_DEVICE_FAULT, "a kernel saw a device-side position outside its table or cache");
+    }
+    return TMAC_OK;
+}
+
+int tmac_step_begin(tmac_context* ctx, tmac_stream stream) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!stream) return fail(ctx, TMAC_ERR_INVALID_ARG, "step_begin: capture needs a created stream, not NULL");
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(ctx, hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return TMAC_OK;
+}
+
+int tmac_step_end(tmac_context* ctx, tmac_stream stream, tmac_graph** graph) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!graph) return fail(ctx, TMAC_ERR_NULL_POINTER, "step_end: null graph handle");
+    hipGraph_t g = nullptr;
+    HIP_TRY(ctx, hipStreamEndCapture((hipStream_t)stream, &g));
+    if (*graph && (*graph)->exec) {
+        hipGraphNode_t err_node = nullptr;
+        hipGraphExecUpdateResult res;
+        if (hipGraphExecUpdate((*graph)->exec, g, &err_node, &res) == hipSuccess &&
+            res == hipGraphExecUpdateSuccess) {
+            (void)hipGraphDestroy(g);
+            return TMAC_OK;
+        }
+        (void)hipGetLastError();
+        (void)hipGraphExecDestroy((*graph)->exec);
+        (*graph)->exec = nullptr;
+    }
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
+    if (!*graph) *graph = new tmac_graph();
+    (*graph)->exec = exec;
+    return TMAC_OK;
+}
+
+int tmac_graph_launch(tmac_context* ctx, tmac_graph* graph, tmac_stream stream) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!graph || !graph->exec) return fail(ctx, TMAC_ERR_NULL_POINTER, "graph_launch: empty graph");
+    HIP_TRY(ctx, hipGraphLaunch(graph->exec, (hipStream_t)stream));
+    return TMAC_OK;
+}
+
+int tmac_graph_destroy(tmac_context* ctx, tmac_graph* graph) {
+    (void)ctx;
+    if (!graph) return TMAC_OK;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    delete graph;
+    return TMAC_OK;
+}
+
+int tmac_malloc(tmac_context* ctx, void** ptr, size_t bytes) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!ptr) return TMAC_ERR_NULL_POINTER;
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(ctx, hipMalloc(ptr, bytes ? bytes : 1));
+    return TMAC_OK;
+}
+
+int tmac_free(tmac_context* ctx, void* ptr) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!ptr) return TMAC_OK;
+    HIP_TRY(ctx, hipFree(ptr));
+    return TMAC_OK;
+}
+
+static int copy_async(tmac_context* ctx, tmac_stream stream, void* dst, const void* src, size_t bytes,
+                      hipMemcpyKind kind) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!bytes) return TMAC_OK;
+    if (!dst || !src) return TMAC_ERR_NULL_POINTER;
+    HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, kind, (hipStream_t)stream));
+    return TMAC_OK;
+}
+
+int tmac_memcpy_h2d(tmac_context* ctx, tmac_stream s, void* d, const void* h, size_t n) {
+    return copy_async(ctx, s, d, h, n, hipMemcpyHostToDevice);
+}
+int tmac_memcpy_d2h(tmac_context* ctx, tmac_stream s, void* h, const void* d, size_t n) {
+    return copy_async(ctx, s, h, d, n, hipMemcpyDeviceToHost);
+}
+int tmac_memcpy_d2d(tmac_context* ctx, tmac_stream s, void* d, const void* src, size_t n) {
+    return copy_async(ctx, s, d, src, n, hipMemcpyDeviceToDevice);
+}
+
+int tmac_memset(tmac_context* ctx, tmac_stream stream, void* dst, int value, size_t bytes) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!bytes) return TMAC_OK;
+    if (!dst) return TMAC_ERR_NULL_POINTER;
+    HIP_TRY(ctx, hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
+    return TMAC_OK;
+}
+
+int tmac_stream_create(tmac_context* ctx, tmac_stream* stream) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!stream) return TMAC_ERR_NULL_POINTER;
+    if ((rc = set_device(ctx))) return rc;
+    hipStream_t s;
+    HIP_TRY(ctx, hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return TMAC_OK;
+}
+
+int tmac_stream_destroy(tmac_context* ctx, tmac_stream stream) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!stream) return TMAC_OK;
+    HIP_TRY(ctx, hipStreamDestroy((hipStream_t)stream));
+    return TMAC_OK;
+}
+
+int tmac_stream_synchronize(tmac_context* ctx, tmac_stream stream) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipStreamSynchronize((hipStream_t)stream));
+    return TMAC_OK;
+}
+
+int tmac_device_synchronize(tmac_context* ctx) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    HIP_TRY(ctx, hipDeviceSynchronize());
+    return TMAC_OK;
+}
+
+int tmac_event_create(tmac_context* ctx, tmac_event* ev) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!ev) return TMAC_ERR_NULL_POINTER;
+    hipEvent_t e;
+    HIP_TRY(ctx, hipEventCreate(&e));
+    *ev = e;
+    return TMAC_OK;
+}
+
+int tmac_event_destroy(tmac_context* ctx, tmac_event ev) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (ev) HIP_TRY(ctx, hipEventDestroy((hipEvent_t)ev));
+    return TMAC_OK;
+}
+
+int tmac_event_record(tmac_context* ctx, tmac_event ev, tmac_stream stream) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipEventRecord((hipEvent_t)ev, (hipStream_t)stream));
+    return TMAC_OK;
+}
+
+int tmac_event_elapsed_ms(tmac_context* ctx, tmac_event start, tmac_event stop, float* ms) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!ms) return TMAC_ERR_NULL_POINTER;
+    HIP_TRY(ctx, hipEventSynchronize((hipEvent_t)stop));
+    HIP_TRY(ctx, hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return TMAC_OK;
+}
+
+int tmac_device_info(tmac_context* ctx, char* buf, size_t buf_len, int* n_cu) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    hipDeviceProp_t p;
+    HIP_TRY(ctx, hipGetDeviceProperties(&p, ctx->device));
+    if (n_cu) *n_cu = p.multiProcessorCount;
+    if (buf && buf_len) {
+        std::snprintf(buf, buf_len,
+                      "{\"name\": \"%s\", \"arch\": \"%s\", \"cu\": %d, \"clock_khz\": %d, "
+                      "\"mem_clock_khz\": %d, \"mem_bus_bits\": %d, \"hbm_bytes\": %zu, \"l2_bytes\": %d}",
+                      p.name, p.gcnArchName, p.multiProcessorCount, p.clockRate, p.memoryClockRate,
+                      p.memoryBusWidth, (size_t)p.totalGlobalMem, p.l2CacheSize);
+    }
+    return TMAC_OK;
+}
+
+}  // extern "C"
