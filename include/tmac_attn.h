@@ -136,11 +136,18 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
 
 /* ---- tuning / introspection ---- */
 enum tmac_option {
-    TMAC_OPT_SPLIT_LEN = 1,   /* rows per workgroup; 0 = automatic (default) */
-    TMAC_OPT_TARGET_GROUPS = 2 /* workgroups the automatic split aims for; 0 = 2 per CU */
+    TMAC_OPT_SPLIT_LEN = 1,     /* group kernel: rows per workgroup; 0 = automatic (default) */
+    TMAC_OPT_TARGET_GROUPS = 2, /* workgroups the automatic split aims for; 0 = one per CU */
+    TMAC_OPT_KERNEL = 3         /* a tmac_kernel_choice */
+};
+enum tmac_kernel_choice {
+    TMAC_KERNEL_AUTO = 0,   /* head kernel for short contexts on few sequences, else group */
+    TMAC_KERNEL_GROUP = 1,  /* workgroup per (split, sequence), each K/V byte read once */
+    TMAC_KERNEL_HEAD = 2    /* workgroup per (query head, sequence), no split merge */
 };
 int tmac_set_option(tmac_context* ctx, int option, int64_t value);
-/* Rows per workgroup the next decode with this shape would use. */
+/* Rows per workgroup and splits the next decode with this shape would use
+ * (*n_splits = 0 means the head kernel). */
 int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_kv_head, int* split_len,
                      int* n_splits);
 /* Reads and clears the device error word (bit 0: bad device-side position, bit 1: ragged length above max_len).

@@ -9,9 +9,21 @@ import numpy as np
 import pytest
 
 import oracle
+import tmac_attn
 from conftest import assert_close
 
 pytestmark = pytest.mark.gpu
+
+KERNELS = {"auto": tmac_attn.TMAC_KERNEL_AUTO, "group": tmac_attn.TMAC_KERNEL_GROUP,
+           "head": tmac_attn.TMAC_KERNEL_HEAD}
+
+
+@pytest.fixture(params=list(KERNELS))
+def kernel(request, ctx):
+    """Runs the test with the automatic choice and with each decode kernel forced."""
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, KERNELS[request.param])
+    yield request.param
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_AUTO)
 
 NH, NKV, HD = 14, 2, 64
 KVD = NKV * HD
@@ -22,7 +34,7 @@ def rand_cache(seed, n_rows, kvd=KVD):
 
 
 @pytest.mark.parametrize("past_len", [0, 1, 7, 8, 15, 16, 31, 32, 33, 63, 100, 255, 256, 1000, 4095])
-def test_attention_op_matches_oracle(ctx, past_len):
+def test_attention_op_matches_oracle(ctx, kernel, past_len):
     n_rows = past_len + 1
     k, v = rand_cache(1000 + past_len, n_rows)
     q = oracle.normal(7 + past_len, NH * HD)
@@ -30,7 +42,7 @@ def test_attention_op_matches_oracle(ctx, past_len):
     dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     dout = ctx.empty(NH * HD)
     ctx.attention_op(dq, dk, dv, dout, NH, NKV, HD, past_len)
-    assert_close(dout.numpy(), ref, f"attention_op past_len={past_len}")
+    assert_close(dout.numpy(), ref, f"attention_op past_len={past_len} kernel={kernel}")
     for d in (dq, dk, dv, dout):
         d.free()
 
@@ -69,7 +81,7 @@ def test_elem_op_cache_write_bit_exact(ctx):
 
 
 @pytest.mark.parametrize("pos", [0, 1, 8, 31, 32, 33, 200, 255])
-def test_layer_attention_matches_reference_sequence(ctx, pos):
+def test_layer_attention_matches_reference_sequence(ctx, kernel, pos):
     """Fused launch == rope_op x2 + elem_op(2) x2 + attention_op (tmac_gguf.cpp:1562-1568)."""
     cap = 256
     k_cache = np.zeros((cap, KVD), np.float32)
@@ -84,14 +96,14 @@ def test_layer_attention_matches_reference_sequence(ctx, pos):
     dkc, dvc = ctx.upload(k_cache), ctx.upload(v_cache)
     dout = ctx.empty(NH * HD)
     ctx.layer_attention(dq, dkn, dvn, dkc, dvc, dout, NH, NKV, HD, pos, cap, 1e6)
-    assert_close(dout.numpy(), ref, f"layer pos={pos}")
+    assert_close(dout.numpy(), ref, f"layer pos={pos} kernel={kernel}")
     np.testing.assert_array_equal(dkc.numpy(), rk)
     np.testing.assert_array_equal(dvc.numpy(), rv)
     np.testing.assert_array_equal(dq.numpy(), q)  # inputs are read only
 
 
 @pytest.mark.parametrize("n_seq,n_pos", [(1, 1), (3, 17), (8, 513), (32, 4096)])
-def test_decode_batched(ctx, n_seq, n_pos):
+def test_decode_batched(ctx, kernel, n_seq, n_pos):
     stride = n_pos + 3
     k = oracle.normal(60 + n_pos, (n_seq * stride, KVD))
     v = oracle.normal(61 + n_pos, (n_seq * stride, KVD))
@@ -102,10 +114,10 @@ def test_decode_batched(ctx, n_seq, n_pos):
     dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     dout = ctx.empty((n_seq, NH * HD))
     ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, stride)
-    assert_close(dout.numpy(), ref, f"batched {n_seq}x{n_pos}")
+    assert_close(dout.numpy(), ref, f"batched {n_seq}x{n_pos} kernel={kernel}")
 
 
-def test_decode_ragged(ctx):
+def test_decode_ragged(ctx, kernel):
     lens = np.array([1, 2, 9, 16, 17, 300, 2048, 5000, 0, 33], np.int32)
     offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
     total = int(lens.sum())
@@ -119,7 +131,7 @@ def test_decode_ragged(ctx):
     doff, dlen = ctx.upload(offs), ctx.upload(lens)
     dout = ctx.empty((lens.size, NH * HD))
     ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, lens.size, NH, NKV, HD, int(lens.max()))
-    assert_close(dout.numpy(), ref, "ragged")
+    assert_close(dout.numpy(), ref, f"ragged kernel={kernel}")
     assert ctx.check_device_error() == 0
 
 

@@ -8,8 +8,12 @@
 namespace tmac {
 
 constexpr int kHeadDim = 64;        // the reference's flash kernel supports only 64 (kernel_flash_attn.metal:18)
-constexpr int kSlotsPerWave = 16;   // 64 lanes = 16 (position, kv-head) slots x 4 dim-lanes
-constexpr int kWavesPerGroup = 4;   // workgroup = 256 threads
+constexpr int kSlotsPerWave = 8;    // 64 lanes = 8 (row, kv-head) slots x 8 dim-lanes
+constexpr int kGroupWaves = 8;      // "group" decode kernel: 512 threads per workgroup
+constexpr int kPrefetchDepth = 3;   // group kernel: steps of K/V in flight per wave (242 VGPRs at G = 7)
+constexpr int kHeadWaves = 16;      // "head" decode kernel (short contexts): 1024 threads
+constexpr int kHeadPrefetchDepth = 2;
+constexpr int kMaxSplits = 256;     // split-KV workgroups per sequence, at most
 constexpr int kPartialStride = kHeadDim + 2;  // per (split, head): acc[64], m, l
 
 // Attention over a KV cache in the reference layout: one row per position,
@@ -27,11 +31,12 @@ struct DecodeArgs {
     int split_len;           // rows per workgroup (multiple of the group's step)
     int n_splits;            // gridDim.x
     float* ws;               // split partials [n_seq][n_splits][n_head][66] (n_splits > 1)
-    int* counters;           // [n_seq] arrival counters, zero between launches
     float qscale;            // log2(e) / sqrt(head_dim): softmax runs in base 2
     // layer mode (RoPE + cache write + attention in one launch)
     const float* k_new;      // [n_kv_head][64] pre-RoPE
     const float* v_new;      // [n_kv_head][64]
+    float* k_out;            // layer cache written at row pos (same memory as k)
+    float* v_out;
     const float2* rope_cs;   // [rope_rows][32] (cos, sin) of pos*theta_j
     const int* pos_dev;      // device-side position (graph replay); null -> pos_host
     int pos_host;

@@ -8,25 +8,27 @@
 //
 // Decode work decomposition (one workgroup = 4 waves = 256 lanes):
 //   * grid = (split, sequence).  A split is a contiguous range of cache rows.
-//   * A wave reads one "step" = 16 slots x 256 B of K and of V per iteration:
-//     slot = (row within step, kv head); with 2 kv heads a step is 8 full
-//     512-B cache rows, i.e. 4 KB of K and 4 KB of V, read with 16-byte loads.
-//   * Each slot is served by 4 lanes; lane c of a slot owns the 16 dims
-//     {16i + 4c + j : i, j in 0..3}, so one 16-byte load instruction covers a
-//     64-byte run of every row it touches.
-//   * Every lane keeps the (pre-scaled) query of all G heads of its kv group
-//     in registers: the K/V row it loads is used by all G = n_head/n_kv_head
-//     query heads of that group without being re-read (GQA sharing).
-//   * q.k partial sums over a lane's 16 dims are reduced across the 4 lanes of
-//     the slot with two DPP quad_perm adds; all 4 lanes end with the same score.
+//   * A wave reads one "step" per iteration: 8 slots x 256 B of K and of V,
+//     slot = (row within the step, kv head).  With 2 kv heads a step is 4 full
+//     512-B cache rows (2 KB of K, 2 KB of V), read with 16-byte loads.
+//   * Each slot is served by 8 lanes; lane c owns the dims {4c..4c+3} and
+//     {32+4c..32+4c+3}, so each 16-byte load instruction covers whole 128-byte
+//     runs of the rows it touches.
+//   * Every lane keeps the pre-scaled query of all G heads of its kv group in
+//     registers: the K/V row it loads serves all G = n_head/n_kv_head query
+//     heads of the group without being re-read (GQA sharing).
+//   * q.k partial sums are reduced over the 8 lanes of a slot with three DPP
+//     adds (quad_perm x2, row_half_mirror); all 8 lanes end with the same score.
 //   * Softmax is online, in base 2, with one running max per (wave, head)
-//     shared by all slots of the wave.  The max is only raised when a score
-//     exceeds it by more than kTau (a wave-uniform, rare branch), so the
-//     common step has no cross-lane traffic besides the two DPP adds.
+//     shared by all slots of the wave.  The max is raised only when a score
+//     exceeds it by more than kTau (a wave-uniform, rare branch), so a common
+//     step has no cross-lane traffic besides the three DPP adds.
+//   * K/V of the next DEPTH-1 steps are in flight while a step is computed.
 //   * End of wave: slots are summed with xor-shuffles (same max, no rescale);
-//     waves are merged in LDS with a log-sum-exp rescale; splits of one
-//     sequence are merged by the last workgroup to arrive (device-scope
-//     fence + atomic counter that the merging workgroup resets to zero).
+//     waves are merged in LDS with a log-sum-exp rescale.  With one split the
+//     workgroup writes the output; otherwise it writes its (m, l, acc) partial
+//     and tmac_combine_* merges the splits in a second, stream-ordered launch
+//     (no device-scope fences or counters inside the decode kernel).
 #include <hip/hip_runtime.h>
 
 #include "attn_args.h"
@@ -37,6 +39,9 @@ namespace {
 
 constexpr float kTau = 8.0f;  // lazy-rescale threshold (log2 units): weights stay <= 2^8
 constexpr float kNegInf = -__builtin_inff();
+constexpr int kLanesPerSlot = 8;
+constexpr int kDimsPerLane = kHeadDim / kLanesPerSlot;  // 8
+constexpr int kSlots = 64 / kLanesPerSlot;              // 8 (row, kv) slots per wave step
 
 enum Mode { kUniform = 0, kRagged = 1, kLayer = 2 };
 
@@ -44,6 +49,14 @@ template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
     return __builtin_bit_cast(
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 8 lanes of a slot; every lane receives the same bits.
+__device__ __forceinline__ float slot_sum(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp<0x141>(x);  // row_half_mirror: lane i <- lane 7-i within each 8-lane half row
+    return x;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -60,40 +73,35 @@ __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float c, float
     x1 = e + f;
 }
 
-// Applies RoPE to a lane's 16 dims {16i + 4c + j} of one head.  Pairs (d, d+1)
-// with d even never straddle a lane: dims 4m..4m+3 hold pairs 2m and 2m+1.
-__device__ __forceinline__ void rope16(float (&x)[16], const float2* __restrict__ cs_row, int c) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 t = *reinterpret_cast<const float4*>(cs_row + 8 * i + 2 * c);
-        rotate_pair(x[4 * i + 0], x[4 * i + 1], t.x, t.y);
-        rotate_pair(x[4 * i + 2], x[4 * i + 3], t.z, t.w);
-    }
+// A lane's 8 dims of one head: x[0..3] = dims 4c..4c+3, x[4..7] = dims 32+4c..32+4c+3.
+__device__ __forceinline__ void load8(float (&x)[8], const float* __restrict__ p) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 32);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
-__device__ __forceinline__ void load16(float (&x)[16], const float* __restrict__ p) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 t = *reinterpret_cast<const float4*>(p + 16 * i);
-        x[4 * i + 0] = t.x;
-        x[4 * i + 1] = t.y;
-        x[4 * i + 2] = t.z;
-        x[4 * i + 3] = t.w;
-    }
+__device__ __forceinline__ void store8(float* __restrict__ p, const float (&x)[8]) {
+    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(p + 32) = make_float4(x[4], x[5], x[6], x[7]);
 }
 
-__device__ __forceinline__ void store16(float* __restrict__ p, const float (&x)[16]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<float4*>(p + 16 * i) =
-            make_float4(x[4 * i + 0], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+// RoPE on a lane's 8 dims.  Pairs (d, d+1), d even, never straddle a lane:
+// dims 4c..4c+3 are pairs 2c, 2c+1 and dims 32+4c.. are pairs 16+2c, 17+2c.
+__device__ __forceinline__ void rope8(float (&x)[8], const float2* __restrict__ cs_row, int c) {
+    const float4 t0 = *reinterpret_cast<const float4*>(cs_row + 2 * c);
+    const float4 t1 = *reinterpret_cast<const float4*>(cs_row + 16 + 2 * c);
+    rotate_pair(x[0], x[1], t0.x, t0.y);
+    rotate_pair(x[2], x[3], t0.z, t0.w);
+    rotate_pair(x[4], x[5], t1.x, t1.y);
+    rotate_pair(x[6], x[7], t1.z, t1.w);
 }
 
 template <int G>
 struct State {
-    float m[G];       // running max (log2 domain), identical in every lane of a kv group
-    float l[G];       // running sum of weights
-    float acc[G][16]; // running sum of weight * v over this lane's 16 dims
+    float m[G];                // running max (log2 domain), identical across a kv group's lanes
+    float l[G];                // running sum of weights
+    float acc[G][kDimsPerLane];// running sum of weight * v over this lane's dims
 };
 
 template <int G>
@@ -103,44 +111,40 @@ __device__ __forceinline__ void state_init(State<G>& st) {
         st.m[g] = kNegInf;
         st.l[g] = 0.f;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) st.acc[g][t] = 0.f;
+        for (int t = 0; t < kDimsPerLane; ++t) st.acc[g][t] = 0.f;
     }
 }
 
-// One step: this lane's slot sees one cache row (kf/vf = its 16 dims of the
-// row's kv head) or nothing (valid == false, only when MASKED).
+// One step: this lane's slot sees one cache row (kf/vf = its 8 dims of the
+// row's kv head) or nothing (valid == false; only when MASKED).
 template <int G, int KV, bool MASKED>
-__device__ __forceinline__ void attend(const float (&q)[G][16], State<G>& st, const float (&kf)[16],
-                                       const float (&vf)[16], bool valid) {
+__device__ __forceinline__ void attend(const float (&q)[G][kDimsPerLane], State<G>& st,
+                                       const float (&kf)[kDimsPerLane], const float (&vf)[kDimsPerLane],
+                                       bool valid) {
     float s[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         float a = q[g][0] * kf[0];
 #pragma unroll
-        for (int t = 1; t < 16; ++t) a = fmaf(q[g][t], kf[t], a);
-        s[g] = a;
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        s[g] += dpp<0xB1>(s[g]);  // quad_perm [1,0,3,2]
-        s[g] += dpp<0x4E>(s[g]);  // quad_perm [2,3,0,1]
+        for (int t = 1; t < kDimsPerLane; ++t) a = fmaf(q[g][t], kf[t], a);
+        s[g] = slot_sum(a);
         if (MASKED) s[g] = valid ? s[g] : kNegInf;
     }
-    bool need = false;
+    float over = s[0] - st.m[0];
 #pragma unroll
-    for (int g = 0; g < G; ++g) need |= (s[g] - st.m[g]) > kTau;
-    if (__any(need)) {
-        // Raise the shared max to the step's max (rare after the first step).
+    for (int g = 1; g < G; ++g) over = fmaxf(over, s[g] - st.m[g]);
+    if (__any(over > kTau)) {
+        // Raise the wave's shared max to this step's max (rare after the first step).
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float mx = s[g];
 #pragma unroll
-            for (int mask = 4 * KV; mask < 64; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
+            for (int mask = kLanesPerSlot * KV; mask < 64; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
             const float mn = fmaxf(st.m[g], mx);
             const float alpha = (st.m[g] == kNegInf) ? 0.f : fast_exp2(st.m[g] - mn);
             st.l[g] *= alpha;
 #pragma unroll
-            for (int t = 0; t < 16; ++t) st.acc[g][t] *= alpha;
+            for (int t = 0; t < kDimsPerLane; ++t) st.acc[g][t] *= alpha;
             st.m[g] = mn;
         }
     }
@@ -149,102 +153,99 @@ __device__ __forceinline__ void attend(const float (&q)[G][16], State<G>& st, co
         const float e = fast_exp2(s[g] - st.m[g]);  // 0 for masked slots (s = -inf)
         st.l[g] += e;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) st.acc[g][t] = fmaf(e, vf[t], st.acc[g][t]);
+        for (int t = 0; t < kDimsPerLane; ++t) st.acc[g][t] = fmaf(e, vf[t], st.acc[g][t]);
     }
 }
 
-// Attends this wave's share of `n_rows` cache rows starting at kb/vb.  Steps
-// are dealt round-robin to the NW waves of the workgroup, so the workgroup
-// streams its range front to back.  One step of K/V is prefetched ahead.
-template <int G, int KV, int NW>
+// Attends this wave's share of `n_rows` cache rows starting at kb/vb.  A step
+// covers PPS = 8/KVS rows x KVS kv heads (ROW floats between rows).  Steps are
+// dealt round-robin to the NW waves of the workgroup (the workgroup streams its
+// range front to back); DEPTH steps of K/V are kept in flight per wave.  Full
+// steps run in the main loop; the one partial step at the end of the range (if
+// any) is loaded and masked after it, so the loop body holds a single copy of
+// the softmax state.
+template <int G, int KVS, int ROW, int NW, int DEPTH>
 __device__ __forceinline__ void attend_rows(const float* __restrict__ kb, const float* __restrict__ vb,
                                             int n_rows, int wave, int lane_off, int lane_row,
-                                            int lane_col, const float (&q)[G][16], State<G>& st) {
-    constexpr int PPS = 16 / KV;       // rows per step
-    constexpr int ROW = KV * kHeadDim; // floats per cache row
-    constexpr int STEP = PPS * ROW;    // floats per step (= 1024)
-    const int full = n_rows / PPS;     // steps whose rows are all in range
-    int t = wave;
-    if (t * PPS >= n_rows) return;
+                                            int lane_col, const float (&q)[G][kDimsPerLane], State<G>& st) {
+    constexpr int PPS = kSlots / KVS;   // rows per step
+    constexpr int STEP = PPS * ROW;     // floats between consecutive steps
+    const int full = n_rows / PPS;      // steps whose rows are all in range
+    const int nk = (full - wave + NW - 1) / NW;  // full steps of this wave: wave + NW*k
 
-    float ka[16], va[16], kb2[16], vb2[16];
-    auto load = [&](int step, float (&kk)[16], float (&vv)[16]) {
-        if (step < full) {
-            const int off = step * STEP + lane_off;
-            load16(kk, kb + off);
-            load16(vv, vb + off);
-        } else {
-            const int r = min(step * PPS + lane_row, n_rows - 1);
-            const int off = r * ROW + lane_col;
-            load16(kk, kb + off);
-            load16(vv, vb + off);
+    if (nk > 0) {
+        float kbuf[DEPTH][kDimsPerLane], vbuf[DEPTH][kDimsPerLane];
+        const float* kp = kb + wave * STEP + lane_off;
+        const float* vp = vb + wave * STEP + lane_off;
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            if (d < nk) {
+                load8(kbuf[d], kp + (size_t)d * NW * STEP);
+                load8(vbuf[d], vp + (size_t)d * NW * STEP);
+            }
         }
-    };
-    auto compute = [&](int step, const float (&kk)[16], const float (&vv)[16]) {
-        if (step < full)
-            attend<G, KV, false>(q, st, kk, vv, true);
-        else
-            attend<G, KV, true>(q, st, kk, vv, step * PPS + lane_row < n_rows);
-    };
-
-    load(t, ka, va);
-    while (true) {
-        int tn = t + NW;
-        bool more = tn * PPS < n_rows;
-        if (more) load(tn, kb2, vb2);
-        compute(t, ka, va);
-        if (!more) break;
-        t = tn;
-        tn = t + NW;
-        more = tn * PPS < n_rows;
-        if (more) load(tn, ka, va);
-        compute(t, kb2, vb2);
-        if (!more) break;
-        t = tn;
+        for (int k0 = 0; k0 < nk; k0 += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                const int k = k0 + d;
+                if (k >= nk) break;
+                attend<G, KVS, false>(q, st, kbuf[d], vbuf[d], true);
+                if (k + DEPTH < nk) {
+                    load8(kbuf[d], kp + (size_t)(k + DEPTH) * NW * STEP);
+                    load8(vbuf[d], vp + (size_t)(k + DEPTH) * NW * STEP);
+                }
+            }
+        }
+    }
+    if (full * PPS < n_rows && (full % NW) == wave) {
+        const int row = full * PPS + lane_row;
+        const int off = min(row, n_rows - 1) * ROW + lane_col;
+        float kf[kDimsPerLane], vf[kDimsPerLane];
+        load8(kf, kb + off);
+        load8(vf, vb + off);
+        attend<G, KVS, true>(q, st, kf, vf, row < n_rows);
     }
 }
 
-// Merges one workgroup's NW wave states; writes either the final output
-// (single split) or this split's partial, then merges splits in the last
-// workgroup to arrive.
-template <int G, int KV, int NW>
-__device__ __forceinline__ void finish(State<G>& st, int lane, int wave, int n_head, int split,
-                                       int n_act, float* __restrict__ out_seq,
-                                       float* __restrict__ ws_seq, int* __restrict__ counter) {
+// Merges one workgroup's NW wave states (KVS*G heads) and writes either the
+// final output (single split) or this split's (acc, m, l) partial.
+template <int G, int KVS, int NW>
+__device__ __forceinline__ void finish(State<G>& st, int lane, int wave, bool direct,
+                                       float* __restrict__ out_heads, float* __restrict__ ws_split) {
+    constexpr int NH = KVS * G;
     // 1. Sum the slots of each kv group inside the wave (they share the max).
 #pragma unroll
-    for (int mask = 4 * KV; mask < 64; mask <<= 1) {
+    for (int mask = kLanesPerSlot * KVS; mask < 64; mask <<= 1) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             st.l[g] += __shfl_xor(st.l[g], mask);
 #pragma unroll
-            for (int t = 0; t < 16; ++t) st.acc[g][t] += __shfl_xor(st.acc[g][t], mask);
+            for (int t = 0; t < kDimsPerLane; ++t) st.acc[g][t] += __shfl_xor(st.acc[g][t], mask);
         }
     }
     // 2. Waves -> LDS.
-    __shared__ float s_acc[NW][KV * G][kHeadDim];
-    __shared__ float s_m[NW][KV * G];
-    __shared__ float s_l[NW][KV * G];
-    __shared__ int s_last;
-    const int slot = lane >> 2, c = lane & 3;
-    if (slot < KV) {  // row 0 of the step holds the wave total for kv head `slot`
-        const int kv = slot;
+    __shared__ float s_acc[NW][NH][kHeadDim];
+    __shared__ float s_m[NW][NH];
+    __shared__ float s_l[NW][NH];
+    const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
+    if (slot < KVS) {  // row 0 of the step holds the wave total for kv slot `slot`
 #pragma unroll
         for (int g = 0; g < G; ++g) {
+            const int h = slot * G + g;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) s_acc[wave][kv * G + g][16 * i + 4 * c + j] = st.acc[g][4 * i + j];
+            for (int j = 0; j < 4; ++j) {
+                s_acc[wave][h][4 * c + j] = st.acc[g][j];
+                s_acc[wave][h][32 + 4 * c + j] = st.acc[g][4 + j];
+            }
             if (c == 0) {
-                s_m[wave][kv * G + g] = st.m[g];
-                s_l[wave][kv * G + g] = st.l[g];
+                s_m[wave][h] = st.m[g];
+                s_l[wave][h] = st.l[g];
             }
         }
     }
     __syncthreads();
-    // 3. Merge waves: thread per (head, dim).
-    const bool direct = (n_act == 1);
-    for (int idx = threadIdx.x; idx < KV * G * kHeadDim; idx += NW * 64) {
+    // 3. Merge waves: one thread per (head, dim).
+    for (int idx = threadIdx.x; idx < NH * kHeadDim; idx += NW * 64) {
         const int h = idx >> 6, d = idx & 63;
         float M = kNegInf;
 #pragma unroll
@@ -258,9 +259,9 @@ __device__ __forceinline__ void finish(State<G>& st, int lane, int wave, int n_h
             A = fmaf(s_acc[w][h][d], sc, A);
         }
         if (direct) {
-            out_seq[idx] = A / L;
+            out_heads[idx] = A / L;
         } else {
-            float* p = ws_seq + ((size_t)split * n_head + h) * kPartialStride;
+            float* p = ws_split + (size_t)h * kPartialStride;
             p[d] = A;
             if (d == 0) {
                 p[kHeadDim] = M;
@@ -268,147 +269,195 @@ __device__ __forceinline__ void finish(State<G>& st, int lane, int wave, int n_h
             }
         }
     }
-    if (direct) return;
-    // 4. Publish this split; the last workgroup of the sequence merges all.
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int prev = atomicAdd(counter, 1);
-        s_last = (prev == n_act - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int idx = threadIdx.x; idx < n_head * kHeadDim; idx += NW * 64) {
-        const int h = idx >> 6, d = idx & 63;
-        float M = kNegInf;
-        for (int sp = 0; sp < n_act; ++sp) M = fmaxf(M, ws_seq[((size_t)sp * n_head + h) * kPartialStride + kHeadDim]);
-        float L = 0.f, A = 0.f;
-        for (int sp = 0; sp < n_act; ++sp) {
-            const float* p = ws_seq + ((size_t)sp * n_head + h) * kPartialStride;
-            const float mw = p[kHeadDim];
-            const float sc = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
-            L = fmaf(p[kHeadDim + 1], sc, L);
-            A = fmaf(p[d], sc, A);
-        }
-        out_seq[idx] = A / L;
-    }
-    if (threadIdx.x == 0) *counter = 0;  // ready for the next launch
 }
 
-template <int G, int KV, int NW, int MODE>
+// Rows attended by sequence `seq` (n_pos) and its cache base, per mode.
+// Returns false for an out-of-range device position.
+template <int KV, int MODE>
+__device__ __forceinline__ bool seq_geometry(const DecodeArgs& a, int seq, int& n_pos, int& pos,
+                                             size_t& base) {
+    constexpr int ROW = KV * kHeadDim;
+    pos = 0;
+    if (MODE == kUniform) {
+        n_pos = a.n_pos;
+        base = (size_t)seq * (size_t)a.seq_stride * ROW;
+    } else if (MODE == kRagged) {
+        n_pos = a.lengths[seq];
+        base = (size_t)a.offsets[seq] * ROW;
+    } else {
+        pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+        if (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) return false;
+        n_pos = pos + 1;
+        base = 0;
+    }
+    return true;
+}
+
+// Decode for one (split, sequence) workgroup.
+//   PER_HEAD = false ("group" kernel): grid (split, seq); every lane carries
+//     the G query heads of its kv head and a step covers all KV kv heads of
+//     PPS = 8/KV rows, so each K/V byte is read from memory once.
+//   PER_HEAD = true ("head" kernel, short contexts): grid (q head, seq), one
+//     split; the workgroup attends all rows for one query head, reading only
+//     its kv head's 256-byte half rows, so no cross-workgroup merge is needed.
+template <int G, int KV, int NW, int DEPTH, int MODE, bool PER_HEAD>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     constexpr int ROW = KV * kHeadDim;
     constexpr int NH = KV * G;
+    constexpr int KVS = PER_HEAD ? 1 : KV;  // kv heads per step
+    constexpr int GW = PER_HEAD ? 1 : G;    // query heads per lane
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int split = blockIdx.x;
+    const int split = PER_HEAD ? 0 : blockIdx.x;
+    const int head = PER_HEAD ? blockIdx.x : 0;
     const int seq = blockIdx.y;
 
-    const float* kseq;
-    const float* vseq;
-    int n_pos, mem_rows, pos = 0;
-    if (MODE == kUniform) {
-        n_pos = a.n_pos;
-        const size_t base = (size_t)seq * (size_t)a.seq_stride * ROW;
-        kseq = a.k + base;
-        vseq = a.v + base;
-        mem_rows = n_pos;
-    } else if (MODE == kRagged) {
-        n_pos = a.lengths[seq];
-        const size_t base = (size_t)a.offsets[seq] * ROW;
-        kseq = a.k + base;
-        vseq = a.v + base;
-        mem_rows = n_pos;
-    } else {
-        pos = a.pos_dev ? *a.pos_dev : a.pos_host;
-        if (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) {
-            if (split == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
-            return;
-        }
-        n_pos = pos + 1;
-        kseq = a.k;
-        vseq = a.v;
-        mem_rows = pos;  // row `pos` is the new token, attended from registers
+    int n_pos, pos;
+    size_t base;
+    if (!seq_geometry<KV, MODE>(a, seq, n_pos, pos, base)) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
+        return;
     }
     float* out_seq = a.out + (size_t)seq * NH * kHeadDim;
+    float* out_heads = out_seq + (PER_HEAD ? head * kHeadDim : 0);
     if (n_pos <= 0) {  // ragged sequence with no rows: defined as a zero output
         if (split == 0)
-            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_seq[i] = 0.f;
+            for (int i = threadIdx.x; i < KVS * GW * kHeadDim; i += NW * 64) out_heads[i] = 0.f;
         return;
     }
     const int n_act = (n_pos + a.split_len - 1) / a.split_len;
     if (n_act > a.n_splits) {  // ragged length above the max_len the grid was sized for
         if (split == 0) {
-            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_seq[i] = __builtin_nanf("");
+            for (int i = threadIdx.x; i < KVS * GW * kHeadDim; i += NW * 64) out_heads[i] = __builtin_nanf("");
             if (threadIdx.x == 0) atomicOr(a.err, 2);
         }
         return;
     }
     if (split >= n_act) return;
+    const int mem_rows = (MODE == kLayer) ? pos : n_pos;  // layer mode: row `pos` comes from registers
     const int r0 = split * a.split_len;
     const int r1 = min(r0 + a.split_len, mem_rows);
 
-    const int slot = lane >> 2, c = lane & 3;
-    const int kv = slot % KV, lane_row = slot / KV;
-    const int lane_col = kv * kHeadDim + 4 * c;
+    const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
+    const int lane_row = slot / KVS;
+    const int kvh = PER_HEAD ? head / G : slot % KVS;  // kv head this lane reads
+    const int lane_col = kvh * kHeadDim + 4 * c;
     const int lane_off = lane_row * ROW + lane_col;
 
-    // Query of the G heads of this lane's kv group, this lane's 16 dims.
-    float q[G][16];
-    const float* qg = a.q + ((size_t)seq * NH + kv * G) * kHeadDim + 4 * c;
+    // Query of this lane's GW heads (its 8 dims), pre-scaled for base-2 softmax.
+    float q[GW][kDimsPerLane];
     const float2* cs_row = nullptr;
     if (MODE == kLayer) cs_row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        load16(q[g], qg + g * kHeadDim);
-        if (MODE == kLayer) rope16(q[g], cs_row, c);
+    for (int g = 0; g < GW; ++g) {
+        const int qh = PER_HEAD ? head : kvh * G + g;
+        load8(q[g], a.q + ((size_t)seq * NH + qh) * kHeadDim + 4 * c);
+        if (MODE == kLayer) rope8(q[g], cs_row, c);
 #pragma unroll
-        for (int t = 0; t < 16; ++t) q[g][t] *= a.qscale;
+        for (int t = 0; t < kDimsPerLane; ++t) q[g][t] *= a.qscale;
     }
 
-    State<G> st;
+    State<GW> st;
     state_init(st);
-    attend_rows<G, KV, NW>(kseq + (size_t)r0 * ROW, vseq + (size_t)r0 * ROW, max(r1 - r0, 0), wave,
-                           lane_off, lane_row, lane_col, q, st);
+    const float* kseq = a.k + base;
+    const float* vseq = a.v + base;
+    attend_rows<GW, KVS, ROW, NW, DEPTH>(kseq + (size_t)r0 * ROW, vseq + (size_t)r0 * ROW, max(r1 - r0, 0),
+                                         wave, lane_off, lane_row, lane_col, q, st);
 
     if (MODE == kLayer && split == n_act - 1 && wave == 0) {
         // The new token (row `pos`): RoPE its k, write k/v to the cache row
-        // (tmac_gguf.cpp:1090-1091) and attend it from registers.
+        // (tmac_gguf.cpp:1090-1091, once per kv head) and attend it from registers.
         const bool mine = (lane_row == 0);
-        float kf[16], vf[16];
+        float kf[kDimsPerLane], vf[kDimsPerLane];
         if (mine) {
-            load16(kf, a.k_new + lane_col);
-            load16(vf, a.v_new + lane_col);
-            rope16(kf, cs_row, c);
-            store16(const_cast<float*>(a.k) + (size_t)pos * ROW + lane_col, kf);
-            store16(const_cast<float*>(a.v) + (size_t)pos * ROW + lane_col, vf);
+            load8(kf, a.k_new + lane_col);
+            load8(vf, a.v_new + lane_col);
+            rope8(kf, cs_row, c);
+            if (!PER_HEAD || head % G == 0) {
+                store8(a.k_out + (size_t)pos * ROW + lane_col, kf);
+                store8(a.v_out + (size_t)pos * ROW + lane_col, vf);
+            }
         } else {
 #pragma unroll
-            for (int t = 0; t < 16; ++t) kf[t] = vf[t] = 0.f;
+            for (int t = 0; t < kDimsPerLane; ++t) kf[t] = vf[t] = 0.f;
         }
-        attend<G, KV, true>(q, st, kf, vf, mine);
+        attend<GW, KVS, true>(q, st, kf, vf, mine);
     }
 
-    float* ws_seq = a.ws ? a.ws + (size_t)seq * a.n_splits * NH * kPartialStride : nullptr;
-    finish<G, KV, NW>(st, lane, wave, NH, split, n_act, out_seq, ws_seq, a.counters ? a.counters + seq : nullptr);
+    const bool direct = (n_act == 1);
+    float* ws_split = direct ? nullptr : a.ws + ((size_t)seq * a.n_splits + split) * NH * kPartialStride;
+    finish<GW, KVS, NW>(st, lane, wave, direct, out_heads, ws_split);
+}
+
+// Log-sum-exp merge of the split partials: one wave per (head, sequence) with
+// more than one active split.  Lanes load the splits' (m, l) in parallel, the
+// per-split weights go to LDS, then lane d sums acc[split][d] in batches of 8
+// independent loads.
+template <int G, int KV, int MODE>
+__device__ __forceinline__ void combine_body(const DecodeArgs& a) {
+    constexpr int NH = KV * G;
+    const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+    int n_pos, pos;
+    size_t base;
+    if (!seq_geometry<KV, MODE>(a, seq, n_pos, pos, base)) return;
+    if (n_pos <= 0) return;
+    const int n_act = (n_pos + a.split_len - 1) / a.split_len;
+    if (n_act <= 1 || n_act > a.n_splits) return;
+    const float* ws = a.ws + (size_t)seq * a.n_splits * NH * kPartialStride + (size_t)h * kPartialStride;
+    constexpr size_t SP = (size_t)NH * kPartialStride;  // floats between splits
+    __shared__ float s_m[kMaxSplits], s_w[kMaxSplits];
+    float mloc = kNegInf;
+    for (int sp = d; sp < n_act; sp += 64) {
+        const float m = ws[sp * SP + kHeadDim];
+        s_m[sp] = m;
+        s_w[sp] = ws[sp * SP + kHeadDim + 1];  // l, replaced by the weight below
+        mloc = fmaxf(mloc, m);
+    }
+#pragma unroll
+    for (int mask = 1; mask < 64; mask <<= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, mask));
+    const float M = mloc;
+    float lsum = 0.f;
+    for (int sp = d; sp < n_act; sp += 64) {
+        const float m = s_m[sp];
+        const float sc = (m == kNegInf) ? 0.f : fast_exp2(m - M);
+        lsum = fmaf(s_w[sp], sc, lsum);
+        s_w[sp] = sc;
+    }
+#pragma unroll
+    for (int mask = 1; mask < 64; mask <<= 1) lsum += __shfl_xor(lsum, mask);
+    __syncthreads();
+    float A = 0.f;
+    int sp = 0;
+    for (; sp + 8 <= n_act; sp += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = ws[(sp + u) * SP + d];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) A = fmaf(v[u], s_w[sp + u], A);
+    }
+    for (; sp < n_act; ++sp) A = fmaf(ws[sp * SP + d], s_w[sp], A);
+    a.out[((size_t)seq * NH + h) * kHeadDim + d] = A / lsum;
 }
 
 }  // namespace
 
-#define TMAC_DECODE_KERNELS(G, KV)                                                          \
-    extern "C" __global__ __launch_bounds__(kWavesPerGroup * 64) void tmac_decode_u_g##G##_kv##KV( \
-        DecodeArgs a) {                                                                     \
-        decode_body<G, KV, kWavesPerGroup, kUniform>(a);                                    \
-    }                                                                                       \
-    extern "C" __global__ __launch_bounds__(kWavesPerGroup * 64) void tmac_decode_r_g##G##_kv##KV( \
-        DecodeArgs a) {                                                                     \
-        decode_body<G, KV, kWavesPerGroup, kRagged>(a);                                     \
-    }                                                                                       \
-    extern "C" __global__ __launch_bounds__(kWavesPerGroup * 64) void tmac_layer_g##G##_kv##KV(    \
-        DecodeArgs a) {                                                                     \
-        decode_body<G, KV, kWavesPerGroup, kLayer>(a);                                      \
+#define TMAC_MODE_KERNELS(G, KV, M, MODE)                                                          \
+    extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_##M##_g##G##_kv##KV(        \
+        DecodeArgs a) {                                                                            \
+        decode_body<G, KV, kGroupWaves, kPrefetchDepth, MODE, false>(a);                           \
+    }                                                                                              \
+    extern "C" __global__ __launch_bounds__(kHeadWaves * 64) void tmac_##M##_head_g##G##_kv##KV(    \
+        DecodeArgs a) {                                                                            \
+        decode_body<G, KV, kHeadWaves, kHeadPrefetchDepth, MODE, true>(a);                         \
+    }                                                                                              \
+    extern "C" __global__ __launch_bounds__(64) void tmac_##M##_combine_g##G##_kv##KV(DecodeArgs a) { \
+        combine_body<G, KV, MODE>(a);                                                              \
     }
+
+#define TMAC_DECODE_KERNELS(G, KV)              \
+    TMAC_MODE_KERNELS(G, KV, decode_u, kUniform) \
+    TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)  \
+    TMAC_MODE_KERNELS(G, KV, layer, kLayer)
 
 // (query heads per kv head, kv heads).  Qwen2-0.5B is (7, 2).
 TMAC_DECODE_KERNELS(7, 2)

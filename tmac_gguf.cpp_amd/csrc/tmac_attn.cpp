@@ -33,12 +33,14 @@ using tmac::PosArgs;
 using tmac::RopeArgs;
 using tmac::kHeadDim;
 using tmac::kPartialStride;
+using tmac::kGroupWaves;
+using tmac::kHeadWaves;
+using tmac::kMaxSplits;
 using tmac::kSlotsPerWave;
-using tmac::kWavesPerGroup;
 
 namespace {
 
-constexpr int kBlock = kWavesPerGroup * 64;
+constexpr int kHeadMaxRows = 1024;  // automatic choice: head kernel up to this many rows
 // (G = n_head / n_kv_head, KV = n_kv_head) pairs compiled into the code object.
 constexpr int kShapes[][2] = {{7, 2}, {1, 1}, {1, 2}, {2, 2}, {4, 2}, {4, 4}, {8, 1}};
 enum { kModeUniform = 0, kModeRagged = 1, kModeLayer = 2 };
@@ -60,16 +62,17 @@ struct tmac_context {
     int device = -1;
     int n_cu = 0;
     hipModule_t module = nullptr;
-    std::map<std::pair<int, int>, hipFunction_t> decode[3];  // by mode, (G, KV)
+    std::map<std::pair<int, int>, hipFunction_t> decode[3];   // group kernel, by mode, (G, KV)
+    std::map<std::pair<int, int>, hipFunction_t> head[3];     // head kernel, same keys
+    std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr;
     float* ws = nullptr;
     size_t ws_floats = 0;
-    int* counters = nullptr;
-    int n_counters = 0;
     int* err = nullptr;
     std::vector<RopeTable> rope;
     int64_t opt_split_len = 0;
     int64_t opt_target_groups = 0;
+    int64_t opt_kernel = TMAC_KERNEL_AUTO;
     std::string last_error;
     char device_name[256] = {0};
 };
@@ -110,9 +113,12 @@ bool capturing(hipStream_t s) {
     return st != hipStreamCaptureStatusNone;
 }
 
+struct Kernels {
+    hipFunction_t group = nullptr, head = nullptr, combine = nullptr;
+};
+
 // Validates the attention shape shared by every decode entry point.
-int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, hipFunction_t* fn_out,
-                int mode) {
+int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kernels* k, int mode) {
     if (head_dim != kHeadDim)
         return fail(ctx, TMAC_ERR_UNSUPPORTED, "head_dim must be 64 (got " + std::to_string(head_dim) + ")");
     if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head != 0)
@@ -123,21 +129,27 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, hipF
         return fail(ctx, TMAC_ERR_UNSUPPORTED,
                     "no kernel for n_head/n_kv_head = " + std::to_string(g) + ", n_kv_head = " +
                         std::to_string(n_kv_head));
-    *fn_out = it->second;
+    if (k) {
+        k->group = it->second;
+        k->head = ctx->head[mode].at({g, n_kv_head});
+        k->combine = ctx->combine[mode].at({g, n_kv_head});
+    }
     return TMAC_OK;
 }
 
-// Rows per workgroup: a multiple of one round of steps over the workgroup
-// (kWavesPerGroup steps of 16/n_kv_head rows); aims for `target` workgroups
-// (2 per CU by default) without going below one round per workgroup.
+// Group kernel: rows per workgroup, a multiple of one round of steps over the
+// workgroup (kGroupWaves steps of 8/n_kv_head rows).  Aims for `target`
+// workgroups (one per CU by default: a 512-thread workgroup at 2 waves per
+// SIMD fills a CU) without going below one round per workgroup, and keeps at
+// most kMaxSplits splits per sequence.
 void choose_split(const tmac_context* ctx, int n_seq, int n_pos, int n_kv_head, int* split_len, int* n_splits) {
-    const int round = kWavesPerGroup * (kSlotsPerWave / n_kv_head);
+    const int round = kGroupWaves * (kSlotsPerWave / n_kv_head);
     const int rounds = (n_pos + round - 1) / round;
     int len;
     if (ctx->opt_split_len > 0) {
         len = (int)(((ctx->opt_split_len + round - 1) / round) * round);
     } else {
-        const int64_t target = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : 2LL * ctx->n_cu;
+        const int64_t target = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : (int64_t)ctx->n_cu;
         int64_t want = (target + n_seq - 1) / (n_seq > 0 ? n_seq : 1);
         if (want < 1) want = 1;
         if (want > rounds) want = rounds;
@@ -145,13 +157,21 @@ void choose_split(const tmac_context* ctx, int n_seq, int n_pos, int n_kv_head, 
         len = (int)(per * round);
     }
     if (len < round) len = round;
+    while ((n_pos + (int64_t)len - 1) / len > kMaxSplits) len += round;
     *split_len = len;
     *n_splits = (n_pos + len - 1) / len;
     if (*n_splits < 1) *n_splits = 1;
 }
 
-int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats, int counters) {
-    if (floats <= ctx->ws_floats && counters <= ctx->n_counters) return TMAC_OK;
+// Head kernel for short contexts that would leave most CUs idle otherwise.
+bool use_head_kernel(const tmac_context* ctx, int n_seq, int n_head, int rows) {
+    if (ctx->opt_kernel == TMAC_KERNEL_HEAD) return true;
+    if (ctx->opt_kernel == TMAC_KERNEL_GROUP) return false;
+    return (int64_t)n_seq * n_head < 2LL * ctx->n_cu && rows <= kHeadMaxRows;
+}
+
+int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats) {
+    if (floats <= ctx->ws_floats) return TMAC_OK;
     if (capturing(stream))
         return fail(ctx, TMAC_ERR_CAPTURE,
                     "split-KV workspace must grow but the stream is capturing; run the same shape once "
@@ -165,17 +185,6 @@ int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats, int c
         if (ctx->ws) (void)hipFree(ctx->ws);
         ctx->ws = p;
         ctx->ws_floats = n;
-    }
-    if (counters > ctx->n_counters) {
-        int n = ctx->n_counters ? ctx->n_counters : 1024;
-        while (n < counters) n *= 2;
-        int* p = nullptr;
-        HIP_TRY(ctx, hipMalloc(&p, (size_t)n * sizeof(int)));
-        HIP_TRY(ctx, hipMemset(p, 0, (size_t)n * sizeof(int)));
-        HIP_TRY(ctx, hipDeviceSynchronize());
-        if (ctx->counters) (void)hipFree(ctx->counters);
-        ctx->counters = p;
-        ctx->n_counters = n;
     }
     return TMAC_OK;
 }
@@ -243,27 +252,34 @@ int launch(tmac_context* ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigne
 
 const float kQScale = (float)(1.4426950408889634 / 8.0);  // log2(e) / sqrt(64)
 
-// Common launch of a decode-family kernel.
-int run_decode(tmac_context* ctx, hipStream_t stream, hipFunction_t fn, DecodeArgs& a, int n_seq,
+// Common launch of a decode-family kernel, plus the split merge when the
+// rows are spread over more than one workgroup per sequence.
+int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeArgs& a, int n_seq,
                int grid_rows, int n_kv_head) {
+    a.qscale = kQScale;
+    a.err = ctx->err;
+    if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
+    if (use_head_kernel(ctx, n_seq, a.n_head, grid_rows)) {
+        a.split_len = grid_rows;
+        a.n_splits = 1;
+        a.ws = nullptr;
+        return launch(ctx, k.head, (unsigned)a.n_head, (unsigned)n_seq, kHeadWaves * 64, stream, &a);
+    }
     int split_len = 0, n_splits = 0;
     choose_split(ctx, n_seq, grid_rows, n_kv_head, &split_len, &n_splits);
     a.split_len = split_len;
     a.n_splits = n_splits;
-    a.qscale = kQScale;
-    a.err = ctx->err;
     if (n_splits > 1) {
         const size_t need = (size_t)n_seq * n_splits * a.n_head * kPartialStride;
-        int rc = ensure_workspace(ctx, stream, need, n_seq);
+        int rc = ensure_workspace(ctx, stream, need);
         if (rc) return rc;
         a.ws = ctx->ws;
-        a.counters = ctx->counters;
     } else {
         a.ws = nullptr;
-        a.counters = nullptr;
     }
-    if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
-    return launch(ctx, fn, (unsigned)n_splits, (unsigned)n_seq, kBlock, stream, &a);
+    int rc = launch(ctx, k.group, (unsigned)n_splits, (unsigned)n_seq, kGroupWaves * 64, stream, &a);
+    if (rc || n_splits == 1) return rc;
+    return launch(ctx, k.combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
 }
 
 }  // namespace
@@ -331,6 +347,14 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->decode[m][{sh[0], sh[1]}] = f;
+            std::snprintf(name, sizeof(name), "%s_head_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
+            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                return bail(hip_fail(ctx, e, name));
+            ctx->head[m][{sh[0], sh[1]}] = f;
+            std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
+            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                return bail(hip_fail(ctx, e, name));
+            ctx->combine[m][{sh[0], sh[1]}] = f;
         }
     }
     if ((e = hipModuleGetFunction(&ctx->k_rope, ctx->module, "tmac_rope")) != hipSuccess ||
@@ -339,7 +363,7 @@ int tmac_init(tmac_context** out, int device) {
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
-    int rc = ensure_workspace(ctx, nullptr, (size_t)1 << 20, 1024);
+    int rc = ensure_workspace(ctx, nullptr, (size_t)1 << 20);
     if (rc) return bail(rc);
     *out = ctx;
     return TMAC_OK;
@@ -352,7 +376,6 @@ int tmac_shutdown(tmac_context* ctx) {
         (void)hipDeviceSynchronize();
         for (auto& t : ctx->rope) (void)hipFree(t.dev);
         if (ctx->ws) (void)hipFree(ctx->ws);
-        if (ctx->counters) (void)hipFree(ctx->counters);
         if (ctx->err) (void)hipFree(ctx->err);
         (void)hipModuleUnload(ctx->module);
     }
@@ -368,8 +391,8 @@ int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, con
     if (!q || !k_cache || !v_cache || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "attention_op: null buffer");
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "attention_op: buffers must be 16-byte aligned");
-    hipFunction_t fn;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeUniform))) return rc;
+    Kernels kern;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeUniform))) return rc;
     if (past_len < 0 || past_len == INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "past_len out of range");
     if ((rc = set_device(ctx))) return rc;
     DecodeArgs a{};
@@ -380,7 +403,7 @@ int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, con
     a.seq_stride = 0;
     a.n_pos = past_len + 1;
     a.n_head = n_head;
-    return run_decode(ctx, (hipStream_t)stream, fn, a, 1, past_len + 1, n_kv_head);
+    return run_decode(ctx, (hipStream_t)stream, kern, a, 1, past_len + 1, n_kv_head);
 }
 
 int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const float* q, const float* k,
@@ -391,8 +414,8 @@ int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const f
     if (!q || !k || !v || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "decode_batched: null buffer");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "decode_batched: buffers must be 16-byte aligned");
-    hipFunction_t fn;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeUniform))) return rc;
+    Kernels kern;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeUniform))) return rc;
     if (n_seq < 0 || n_pos < 1 || seq_stride < 0 || (n_seq > 1 && seq_stride < n_pos))
         return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_batched: need n_seq >= 0, n_pos >= 1, seq_stride >= n_pos");
     if (n_seq == 0) return TMAC_OK;
@@ -405,7 +428,7 @@ int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const f
     a.seq_stride = seq_stride;
     a.n_pos = n_pos;
     a.n_head = n_head;
-    return run_decode(ctx, (hipStream_t)stream, fn, a, n_seq, n_pos, n_kv_head);
+    return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, n_pos, n_kv_head);
 }
 
 int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const float* q,
@@ -418,8 +441,8 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
         return fail(ctx, TMAC_ERR_NULL_POINTER, "decode_ragged: null buffer");
     if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "decode_ragged: buffers must be 16-byte aligned");
-    hipFunction_t fn;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeRagged))) return rc;
+    Kernels kern;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeRagged))) return rc;
     if (n_seq < 0 || max_len < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: need max_len >= 1");
     if (n_seq == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
@@ -431,7 +454,7 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
     a.offsets = offsets;
     a.lengths = lengths;
     a.n_head = n_head;
-    return run_decode(ctx, (hipStream_t)stream, fn, a, n_seq, max_len, n_kv_head);
+    return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head);
 }
 
 static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, const float* k_new,
@@ -445,8 +468,8 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
     if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new) || !aligned16(k_cache) ||
         !aligned16(v_cache) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "layer_attention: buffers must be 16-byte aligned");
-    hipFunction_t fn;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &fn, kModeLayer))) return rc;
+    Kernels kern;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeLayer))) return rc;
     if (capacity < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "layer_attention: capacity < 1");
     if (!pos_dev && (pos < 0 || pos >= capacity))
         return fail(ctx, TMAC_ERR_CAPACITY, "layer_attention: pos outside [0, capacity)");
@@ -462,12 +485,14 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
     a.n_head = n_head;
     a.k_new = k_new;
     a.v_new = v_new;
+    a.k_out = k_cache;
+    a.v_out = v_cache;
     a.rope_cs = rt->dev;
     a.rope_rows = rt->rows;
     a.pos_dev = pos_dev;
     a.pos_host = pos;
     a.capacity = capacity;
-    return run_decode(ctx, stream, fn, a, 1, pos_dev ? capacity : pos + 1, n_kv_head);
+    return run_decode(ctx, stream, kern, a, 1, pos_dev ? capacity : pos + 1, n_kv_head);
 }
 
 int tmac_layer_attention(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_new,
@@ -544,6 +569,10 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
     switch (option) {
         case TMAC_OPT_SPLIT_LEN: ctx->opt_split_len = value; return TMAC_OK;
         case TMAC_OPT_TARGET_GROUPS: ctx->opt_target_groups = value; return TMAC_OK;
+        case TMAC_OPT_KERNEL:
+            if (value > TMAC_KERNEL_HEAD) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: bad kernel choice");
+            ctx->opt_kernel = value;
+            return TMAC_OK;
         default: return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: unknown option");
     }
 }
@@ -553,9 +582,13 @@ int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if (!split_len || !n_splits) return TMAC_ERR_NULL_POINTER;
-    hipFunction_t fn;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, kHeadDim, &fn, kModeUniform))) return rc;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, kHeadDim, nullptr, kModeUniform))) return rc;
     if (n_seq < 1 || n_pos < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "query_split: n_seq, n_pos >= 1");
+    if (use_head_kernel(ctx, n_seq, n_head, n_pos)) {
+        *split_len = n_pos;
+        *n_splits = 0;  // 0 = head kernel (one workgroup per query head)
+        return TMAC_OK;
+    }
     choose_split(ctx, n_seq, n_pos, n_kv_head, split_len, n_splits);
     return TMAC_OK;
 }

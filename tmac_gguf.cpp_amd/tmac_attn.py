@@ -34,6 +34,10 @@ TMAC_ERR_HIP_BASE = 1000
 
 TMAC_OPT_SPLIT_LEN = 1
 TMAC_OPT_TARGET_GROUPS = 2
+TMAC_OPT_KERNEL = 3
+TMAC_KERNEL_AUTO = 0
+TMAC_KERNEL_GROUP = 1
+TMAC_KERNEL_HEAD = 2
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
