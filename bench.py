@@ -284,6 +284,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--only-c3", action="store_true", help="time config 3 only (for profiling)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run plain 256 MiB device-to-device copies (counter calibration)")
     ap.add_argument("--sections", default="c1,c2,c4",
                     help="extra sections to run besides config 3: any of c1,c2,c2eager,c4")
     args = ap.parse_args()
@@ -297,6 +299,16 @@ def main():
     log(f"[bench] device {info}")
     stream = ctx.stream()
 
+    if args.copy_calib:
+        n = 256 << 20
+        a, b = ctx.empty(n // 4), ctx.empty(n // 4)
+        a.fill_bytes(1, stream)
+        for _ in range(3):
+            ctx._check(ctx.lib.tmac_memcpy_d2d(ctx.handle, stream, b.ptr, a.ptr, n), "memcpy_d2d")
+        ctx.synchronize(stream)
+        a.free()
+        b.free()
+        log(f"[bench] copy calibration: 3 x {n} B device-to-device")
     c3, c3_data = bench_c3(ctx, stream, args.steps, args.warmup)
     log(f"[bench] C3 {c3['gbs']:.1f} GB/s, {c3['mean_ms'] * 1e3:.1f} us/launch, split {c3['split_len']}x{c3['n_splits']}")
     extra = {}

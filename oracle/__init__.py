@@ -50,6 +50,10 @@ def _load(path: str) -> ctypes.CDLL:
     lib.tmac_fill_normal.restype = None
     lib.tmac_splitmix64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
     lib.tmac_splitmix64.restype = ctypes.c_uint64
+    lib.tmac_rng_set_state.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64)]
+    lib.tmac_rng_set_state.restype = None
+    lib.tmac_rng_next.argtypes = [ctypes.c_void_p]
+    lib.tmac_rng_next.restype = ctypes.c_uint64
     lib.oracle_rope_heads.argtypes = [_F, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float]
     lib.oracle_rope_heads.restype = None
     lib.oracle_rope_theta.argtypes = [_F, ctypes.c_int, ctypes.c_float]
@@ -91,6 +95,14 @@ def normal(seed: int, shape) -> np.ndarray:
     return out
 
 
+def xoshiro256ss(state, n: int) -> list[int]:
+    """First n outputs of xoshiro256** from the raw 4-word state."""
+    buf = ctypes.create_string_buffer(64)  # tmac_rng: 4 x u64 + int + double
+    st = (ctypes.c_uint64 * 4)(*state)
+    lib().tmac_rng_set_state(buf, st)
+    return [lib().tmac_rng_next(buf) for _ in range(n)]
+
+
 def splitmix64(state: int, n: int) -> list[int]:
     st = ctypes.c_uint64(state)
     return [lib().tmac_splitmix64(ctypes.byref(st)) for _ in range(n)]
@@ -127,7 +139,8 @@ def attention(q, k_cache, v_cache, n_head: int, n_kv_head: int, head_dim: int, p
     q = _f32(q)
     k_cache = _f32(k_cache)
     v_cache = _f32(v_cache)
-    assert k_cache.size >= (past_len + 1) * n_kv_head * head_dim
+    if past_len < 0 or k_cache.size < (past_len + 1) * n_kv_head * head_dim or v_cache.size < k_cache.size:
+        raise ValueError("oracle_attention: cache smaller than past_len + 1 rows")
     out = np.empty(n_head * head_dim, dtype=np.float32)
     rc = lib().oracle_attention(_fp(q), _fp(k_cache), _fp(v_cache), _fp(out),
                                 n_head, n_kv_head, head_dim, past_len)

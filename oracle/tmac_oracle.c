@@ -36,6 +36,12 @@ void tmac_rng_seed(tmac_rng* r, uint64_t seed) {
     r->spare = 0.0;
 }
 
+void tmac_rng_set_state(tmac_rng* r, const uint64_t state[4]) {
+    for (int i = 0; i < 4; i++) r->s[i] = state[i];
+    r->has_spare = 0;
+    r->spare = 0.0;
+}
+
 uint64_t tmac_rng_next(tmac_rng* r) {
     uint64_t* s = r->s;
     const uint64_t result = rotl64(s[1] * 5, 7) * 9;

@@ -40,6 +40,7 @@ typedef struct {
 uint64_t tmac_splitmix64(uint64_t* state);
 void tmac_rng_seed(tmac_rng* r, uint64_t seed);
 uint64_t tmac_rng_next(tmac_rng* r);
+void tmac_rng_set_state(tmac_rng* r, const uint64_t state[4]);  /* raw state (test vectors) */
 double tmac_rng_uniform(tmac_rng* r);                  /* [0, 1), 53 random bits */
 void tmac_rng_normal_f32(tmac_rng* r, float* out, size_t n);
 /* Convenience: fill `out` with n N(0,1) floats from a fresh stream `seed`. */

@@ -1,0 +1,60 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+include/tmac_attn.h declares, and rejects calls without a context before
+touching the device."""
+import ctypes
+import subprocess
+
+import pytest
+
+import tmac_attn
+
+
+def test_library_loads_and_reports_version():
+    lib = tmac_attn.load_library()
+    assert lib.tmac_abi_version() == 1
+
+
+def test_every_declared_symbol_is_exported():
+    declared = tmac_attn.declared_symbols()
+    assert len(declared) >= 30
+    out = subprocess.run(["nm", "-D", "--defined-only", tmac_attn.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    # and the Python front end binds exactly the declared set
+    assert sorted(tmac_attn.SIGNATURES) == declared
+
+
+def test_status_strings():
+    assert tmac_attn.status_string(0) == "ok"
+    assert "unsupported" in tmac_attn.status_string(tmac_attn.TMAC_ERR_UNSUPPORTED)
+    assert tmac_attn.status_string(424242) == "unknown status" or tmac_attn.status_string(424242)
+
+
+def test_calls_without_context_are_rejected():
+    lib = tmac_attn.load_library()
+    nc = tmac_attn.TMAC_ERR_NOT_INITIALIZED
+    assert lib.tmac_attention_op(None, None, 16, 16, 16, 16, 14, 2, 64, 0) == nc
+    assert lib.tmac_rope_op(None, None, 16, 14, 64, 0, 1e6) == nc
+    assert lib.tmac_elem_op(None, None, 2, 16, 16, 128) == nc
+    assert lib.tmac_layer_attention(None, None, 16, 16, 16, 16, 16, 16, 14, 2, 64, 0, 256, 1e6) == nc
+    assert lib.tmac_attention_decode_batched(None, None, 16, 16, 16, 16, 1, 14, 2, 64, 1, 1) == nc
+    assert lib.tmac_attention_decode_ragged(None, None, 16, 16, 16, 16, 16, 16, 1, 14, 2, 64, 1) == nc
+    assert lib.tmac_step_begin(None, None) == nc
+    assert lib.tmac_malloc(None, ctypes.byref(ctypes.c_void_p()), 16) == nc
+    assert lib.tmac_shutdown(None) == nc
+
+
+def test_init_without_gpu_fails_cleanly():
+    """In a container without a GPU, tmac_init must fail with a HIP status, not crash
+    or fall back to the CPU."""
+    lib = tmac_attn.load_library()
+    h = ctypes.c_void_p()
+    rc = lib.tmac_init(ctypes.byref(h), 0)
+    if rc == tmac_attn.TMAC_OK:  # running on a GPU box
+        lib.tmac_shutdown(h)
+        pytest.skip("a GPU is present")
+    assert rc >= tmac_attn.TMAC_ERR_HIP_BASE or rc in (tmac_attn.TMAC_ERR_INVALID_ARG,
+                                                      tmac_attn.TMAC_ERR_UNSUPPORTED)
+    assert h.value is None
