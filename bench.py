@@ -227,6 +227,32 @@ def bench_c4(ctx, stream, steps, warmup, n_seq=16, max_len=32768):
             "gbs": nbytes / (mean_ms * 1e-3) / 1e9, "pct_of_peak": nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS * 100}
 
 
+C5_FLOPS = 13_157_007_360  # 4 seqs x 14 heads x sum_{i<512} (1537 + i) rows x 4*64 flop (QK^T + PV)
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
+    """Config 5: chunked causal prefill on bf16 MFMA."""
+    cap = prefix + n_q
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((n_seq, n_q, NH * HD), dtype=np.float32)
+    k = rng.standard_normal((n_seq, cap, KVD), dtype=np.float32)
+    v = rng.standard_normal((n_seq, cap, KVD), dtype=np.float32)
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    dout = ctx.empty((n_seq, n_q, NH * HD))
+
+    def launch():
+        ctx.prefill(dq, dk, dv, dout, n_seq, n_q, prefix, cap, NH, NKV, HD, stream=stream)
+
+    per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
+    for d in (dq, dk, dv, dout):
+        d.free()
+    tflops = C5_FLOPS / (mean_ms * 1e-3) / 1e12
+    return {"mean_us": mean_ms * 1e3, "median_us": float(np.median(per)) * 1e3, "flops": C5_FLOPS,
+            "tflops": tflops, "mfma_util": tflops / MFMA_BF16_PEAK_TFLOPS,
+            "bytes": n_seq * n_q * NH * HD * 4 * 2 + n_seq * cap * KVD * 4 * 2}
+
+
 def cpu_baseline(c3_data, budget_s: float = 10.0):
     """The reference CPU attention path (oracle/, -O3 build, one thread) timed
     on a sample of the config-3 batch; the same sequences' GPU outputs are
@@ -286,8 +312,8 @@ def main():
     ap.add_argument("--only-c3", action="store_true", help="time config 3 only (for profiling)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
-    ap.add_argument("--sections", default="c1,c2,c4",
-                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4")
+    ap.add_argument("--sections", default="c1,c2,c4,c5",
+                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -322,6 +348,10 @@ def main():
     if "c4" in sections:
         extra["c4"] = bench_c4(ctx, stream, max(10, args.steps // 2), args.warmup)
         log(f"[bench] C4 {extra['c4']['gbs']:.1f} GB/s")
+    if "c5" in sections:
+        extra["c5"] = bench_c5(ctx, stream, max(10, args.steps // 2), args.warmup)
+        log(f"[bench] C5 {extra['c5']['mean_us']:.1f} us, {extra['c5']['tflops']:.1f} TFLOP/s, "
+            f"MFMA util {extra['c5']['mfma_util'] * 100:.2f}%")
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

@@ -134,6 +134,18 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
                                  const int32_t* lengths, float* out, int n_seq, int n_head,
                                  int n_kv_head, int head_dim, int max_len);
 
+/* ---- chunked causal prefill (extension; the reference feeds prompts one token at a time,
+ *      tmac_gguf.cpp:1621-1658, so its oracle is attention_op per query row) ----
+ * Query i of sequence s sits at position prefix_len + i and attends rows
+ * 0..prefix_len + i of that sequence's cache (rows prefix_len.. must already
+ * hold the chunk's rotated k and v).  q/out [n_seq][n_q][n_head][64]; sequence s
+ * starts at row s * seq_stride.  QK^T and PV run on bf16 MFMA (q, k, v rounded
+ * to bf16, fp32 accumulation, P split into bf16 hi + lo); with bf16-exact
+ * inputs the result matches the fp32 CPU path within the fp32 tolerance. */
+int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
+                           const float* v_cache, float* out, int n_seq, int n_q, int prefix_len,
+                           int64_t seq_stride, int n_head, int n_kv_head, int head_dim);
+
 /* ---- tuning / introspection ---- */
 enum tmac_option {
     TMAC_OPT_SPLIT_LEN = 1,     /* group kernel: rows per workgroup; 0 = automatic (default) */

@@ -45,6 +45,22 @@ struct DecodeArgs {
     int* err;                // device error word (bit 0: position out of range)
 };
 
+// Chunked causal prefill: query i of sequence s sits at absolute position
+// prefix_len + i and attends cache rows 0..prefix_len + i of that sequence.
+struct PrefillArgs {
+    const float* q;          // [n_seq][n_q][n_head][64]
+    const float* k;          // sequence s starts at row s * seq_stride; row = [n_kv_head][64]
+    const float* v;
+    float* out;              // [n_seq][n_q][n_head][64]
+    int64_t seq_stride;
+    int n_q;
+    int prefix_len;
+    float qscale;            // log2(e) / sqrt(head_dim)
+};
+constexpr int kPrefillQueries = 16;  // queries per workgroup (one MFMA column block)
+constexpr int kPrefillKeys = 64;     // keys per LDS tile
+constexpr int kPrefillWaves = 8;     // waves per workgroup (G <= 8 compute, all load)
+
 struct RopeArgs {
     float* x;                // [n_heads][64], rotated in place
     const float2* rope_cs;   // [rope_rows][32]

@@ -468,6 +468,194 @@ TMAC_DECODE_KERNELS(4, 2)
 TMAC_DECODE_KERNELS(4, 4)
 TMAC_DECODE_KERNELS(8, 1)
 
+// ---------------------------------------------------------------------------
+// Chunked causal prefill on bf16 MFMA (v_mfma_f32_16x16x32_bf16).
+//
+// Workgroup = (16-query block, kv head, sequence), 8 waves; wave w < G owns
+// query head kv*G + w.  Per 64-key tile all 512 lanes load K and V (fp32) for
+// the kv head, convert to bf16 (round to nearest even) and stage K as
+// [key][dim] and V as V^T [dim][key] in LDS (rows padded to 72 bf16), shared
+// by the G heads of the group.  Each compute wave works transposed:
+//   S^T (64 keys x 16 queries) = K (keys x dims) . Q^T        8 MFMAs
+//   O^T (64 dims x 16 queries) += V^T (dims x keys) . P^T    16 MFMAs
+// so lane l owns query column l%16 in every accumulator and the online
+// softmax (max, rescale, row sum) is lane-local except for two xor shuffles
+// per tile.  P is split into bf16 hi + lo parts (two PV MFMAs), which keeps
+// the weights to ~2^-17 relative error; with bf16-representable q/k/v the
+// result matches an fp32 evaluation to fp32 rounding.  The key order inside
+// each PV K-step is a permutation shared by the V^T and P^T operands, which
+// leaves the contraction unchanged.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileStride = 72;  // bf16 per LDS row (64 + 8 pad: conflict-free 16-byte reads)
+
+template <int G, int KV>
+__device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
+    constexpr int ROW = KV * kHeadDim;
+    constexpr int NH = KV * G;
+    constexpr int QB = kPrefillQueries, KT = kPrefillKeys;
+    static_assert(G <= kPrefillWaves, "one compute wave per query head of the group");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qblk = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z;
+    const int q0 = qblk * QB;
+    if (q0 >= a.n_q) return;
+    const int q_last = min(q0 + QB, a.n_q) - 1;
+    const int kmax = a.prefix_len + q_last;          // last key any query of the block attends
+    const int n_tiles = kmax / KT + 1;
+    const float* kseq = a.k + (size_t)seq * a.seq_stride * ROW + kv * kHeadDim;
+    const float* vseq = a.v + (size_t)seq * a.seq_stride * ROW + kv * kHeadDim;
+
+    __shared__ __bf16 s_k[KT * kTileStride];   // [key][dim]
+    __shared__ __bf16 s_vt[kHeadDim * kTileStride];  // [dim][key]
+
+    const int col = lane & 15;   // query column / MFMA row index
+    const int g4 = lane >> 4;    // k-group of the MFMA operands
+    const bool compute = wave < G;
+    const int head = kv * G + (compute ? wave : 0);
+    const int qi = q0 + col;
+    const int ap = a.prefix_len + qi;  // absolute position of this lane's query
+
+    // Q^T operand: this lane's query, dims 32j + 8*g4 + (0..7), j = 0, 1.
+    bf16x8 qop[2];
+    {
+        const float* qp = a.q + (((size_t)seq * a.n_q + min(qi, a.n_q - 1)) * NH + head) * kHeadDim;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * j + 8 * g4);
+            const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * j + 8 * g4 + 4);
+            qop[j][0] = (__bf16)x0.x; qop[j][1] = (__bf16)x0.y; qop[j][2] = (__bf16)x0.z; qop[j][3] = (__bf16)x0.w;
+            qop[j][4] = (__bf16)x1.x; qop[j][5] = (__bf16)x1.y; qop[j][6] = (__bf16)x1.z; qop[j][7] = (__bf16)x1.w;
+        }
+    }
+
+    f32x4 o[4];  // O^T blocks: dims 16*db + 4*g4 + i, query col
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = kNegInf, lsum = 0.f;
+
+    // Tile loaders: K as 2 float4 per thread, V as a key pair x float4.
+    const int kf0 = tid, kf1 = tid + 512;  // float4 index = key * 16 + col4
+    const int vpair = tid >> 4, vcol4 = tid & 15;
+    float4 kr0, kr1, vr0, vr1;
+    auto load_tile = [&](int t) {
+        const int base = t * KT;
+        const int k0 = min(base + (kf0 >> 4), kmax), k1 = min(base + (kf1 >> 4), kmax);
+        kr0 = *reinterpret_cast<const float4*>(kseq + (size_t)k0 * ROW + 4 * (kf0 & 15));
+        kr1 = *reinterpret_cast<const float4*>(kseq + (size_t)k1 * ROW + 4 * (kf1 & 15));
+        const int v0 = min(base + 2 * vpair, kmax), v1 = min(base + 2 * vpair + 1, kmax);
+        vr0 = *reinterpret_cast<const float4*>(vseq + (size_t)v0 * ROW + 4 * vcol4);
+        vr1 = *reinterpret_cast<const float4*>(vseq + (size_t)v1 * ROW + 4 * vcol4);
+    };
+    auto store_tile = [&]() {
+        bf16x4 k0v = {(__bf16)kr0.x, (__bf16)kr0.y, (__bf16)kr0.z, (__bf16)kr0.w};
+        bf16x4 k1v = {(__bf16)kr1.x, (__bf16)kr1.y, (__bf16)kr1.z, (__bf16)kr1.w};
+        *reinterpret_cast<bf16x4*>(&s_k[(kf0 >> 4) * kTileStride + 4 * (kf0 & 15)]) = k0v;
+        *reinterpret_cast<bf16x4*>(&s_k[(kf1 >> 4) * kTileStride + 4 * (kf1 & 15)]) = k1v;
+        const float a0[4] = {vr0.x, vr0.y, vr0.z, vr0.w}, a1[4] = {vr1.x, vr1.y, vr1.z, vr1.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+            bf16x2 pr = {(__bf16)a0[i], (__bf16)a1[i]};
+            *reinterpret_cast<bf16x2*>(&s_vt[(4 * vcol4 + i) * kTileStride + 2 * vpair]) = pr;
+        }
+    };
+
+    load_tile(0);
+    for (int t = 0; t < n_tiles; ++t) {
+        __syncthreads();  // previous tile's LDS reads are done
+        store_tile();
+        __syncthreads();
+        if (t + 1 < n_tiles) load_tile(t + 1);  // in flight during this tile's MFMAs
+        if (compute) {
+            // S^T = K . Q^T
+            f32x4 st[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                st[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(
+                        &s_k[(16 * kb + col) * kTileStride + 32 * j + 8 * g4]);
+                    st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[j], st[kb], 0, 0, 0);
+                }
+            }
+            // scale, causal mask, online softmax for query `col`
+            const int kbase = t * KT;
+            const bool diag = kbase + KT - 1 > a.prefix_len + q0;  // tile reaches past some query
+            float tmax = kNegInf;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float sv = st[kb][i] * a.qscale;
+                    if (diag && kbase + 16 * kb + 4 * g4 + i > ap) sv = kNegInf;
+                    st[kb][i] = sv;
+                    tmax = fmaxf(tmax, sv);
+                }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float mn = fmaxf(m, tmax);
+            const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
+            m = mn;
+            lsum *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+            // P^T operands (hi, lo) for the two PV K-steps: keys 32j + 4*g4 + i, 32j + 16 + 4*g4 + i
+            bf16x8 ph[2], pl[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float p = fast_exp2(st[2 * j + h][i] - mn);
+                        lsum += p;
+                        const __bf16 hi = (__bf16)p;
+                        ph[j][4 * h + i] = hi;
+                        pl[j][4 * h + i] = (__bf16)(p - (float)hi);
+                    }
+            // O^T += V^T . P^T
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const __bf16* vrow = &s_vt[(16 * db + col) * kTileStride + 32 * j + 4 * g4];
+                    const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow);
+                    const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + 16);
+                    const bf16x8 vop = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, ph[j], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pl[j], o[db], 0, 0, 0);
+                }
+            }
+        }
+    }
+    if (!compute || qi >= a.n_q) return;
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    const float inv = 1.f / lsum;
+    float* op = a.out + (((size_t)seq * a.n_q + qi) * NH + head) * kHeadDim + 4 * g4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+        *reinterpret_cast<float4*>(op + 16 * db) =
+            make_float4(o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv);
+}
+
+#define TMAC_PREFILL_KERNEL(G, KV)                                                                    \
+    extern "C" __global__ __launch_bounds__(kPrefillWaves * 64) void tmac_prefill_g##G##_kv##KV(      \
+        PrefillArgs a) {                                                                              \
+        prefill_body<G, KV>(a);                                                                       \
+    }
+TMAC_PREFILL_KERNEL(7, 2)
+TMAC_PREFILL_KERNEL(1, 1)
+TMAC_PREFILL_KERNEL(1, 2)
+TMAC_PREFILL_KERNEL(2, 2)
+TMAC_PREFILL_KERNEL(4, 2)
+TMAC_PREFILL_KERNEL(4, 4)
+TMAC_PREFILL_KERNEL(8, 1)
+
 // RoPE in place, one lane per (head, pair): tmac_gguf.cpp:992-1003 for one
 // tensor, i.e. what rope_op (metal_backend.hpp:381) dispatches.
 extern "C" __global__ __launch_bounds__(256) void tmac_rope(RopeArgs a) {

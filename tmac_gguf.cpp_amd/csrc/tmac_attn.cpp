@@ -29,6 +29,9 @@ extern "C" const uint64_t tmac_attn_code_object_size;
 
 using tmac::CopyArgs;
 using tmac::DecodeArgs;
+using tmac::PrefillArgs;
+using tmac::kPrefillQueries;
+using tmac::kPrefillWaves;
 using tmac::PosArgs;
 using tmac::RopeArgs;
 using tmac::kHeadDim;
@@ -65,6 +68,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> decode[3];   // group kernel, by mode, (G, KV)
     std::map<std::pair<int, int>, hipFunction_t> head[3];     // head kernel, same keys
     std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
+    std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr;
     float* ws = nullptr;
     size_t ws_floats = 0;
@@ -244,9 +248,9 @@ int rope_table(tmac_context* ctx, hipStream_t stream, int head_dim, float base, 
 }
 
 int launch(tmac_context* ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned block, hipStream_t stream,
-           void* args) {
+           void* args, unsigned gz = 1) {
     void* params[] = {args};
-    HIP_TRY(ctx, hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, 0, stream, params, nullptr));
+    HIP_TRY(ctx, hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, 0, stream, params, nullptr));
     return TMAC_OK;
 }
 
@@ -355,6 +359,12 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->combine[m][{sh[0], sh[1]}] = f;
+            if (m == 0) {
+                std::snprintf(name, sizeof(name), "tmac_prefill_g%d_kv%d", sh[0], sh[1]);
+                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                    return bail(hip_fail(ctx, e, name));
+                ctx->prefill[{sh[0], sh[1]}] = f;
+            }
         }
     }
     if ((e = hipModuleGetFunction(&ctx->k_rope, ctx->module, "tmac_rope")) != hipSuccess ||
@@ -509,6 +519,29 @@ int tmac_layer_attention_devpos(tmac_context* ctx, tmac_stream stream, const flo
     if (!pos_dev) return fail(ctx, TMAC_ERR_NULL_POINTER, "layer_attention_devpos: null pos_dev");
     return layer_common(ctx, (hipStream_t)stream, q, k_new, v_new, k_cache, v_cache, out, n_head,
                         n_kv_head, head_dim, 0, pos_dev, capacity, base);
+}
+
+int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
+                           const float* v_cache, float* out, int n_seq, int n_q, int prefix_len,
+                           int64_t seq_stride, int n_head, int n_kv_head, int head_dim) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !k_cache || !v_cache || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "prefill: null buffer");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "prefill: buffers must be 16-byte aligned");
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, nullptr, kModeUniform))) return rc;
+    if (n_seq < 0 || n_q < 0 || prefix_len < 0 || (int64_t)prefix_len + n_q > INT_MAX)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: need n_seq, n_q, prefix_len >= 0");
+    if (n_seq > 1 && seq_stride < (int64_t)prefix_len + n_q)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: seq_stride must cover prefix_len + n_q rows");
+    if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: n_seq exceeds 65535");
+    if (n_seq == 0 || n_q == 0) return TMAC_OK;
+    auto it = ctx->prefill.find({n_head / n_kv_head, n_kv_head});
+    if (it == ctx->prefill.end()) return fail(ctx, TMAC_ERR_UNSUPPORTED, "prefill: unsupported group");
+    if ((rc = set_device(ctx))) return rc;
+    PrefillArgs a{q, k_cache, v_cache, out, seq_stride, n_q, prefix_len, kQScale};
+    return launch(ctx, it->second, (unsigned)((n_q + kPrefillQueries - 1) / kPrefillQueries), (unsigned)n_kv_head,
+                  kPrefillWaves * 64, (hipStream_t)stream, &a, (unsigned)n_seq);
 }
 
 int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add) {
