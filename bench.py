@@ -310,6 +310,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--only-c3", action="store_true", help="time config 3 only (for profiling)")
+    ap.add_argument("--rotate", type=int, default=None, help="override TMAC_OPT_ROTATE (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
     ap.add_argument("--sections", default="c1,c2,c4,c5",
@@ -324,6 +325,8 @@ def main():
     info, n_cu = ctx.device_info()
     log(f"[bench] device {info}")
     stream = ctx.stream()
+    if args.rotate is not None:
+        ctx.set_option(tmac_attn.TMAC_OPT_ROTATE, args.rotate)
 
     if args.copy_calib:
         n = 256 << 20

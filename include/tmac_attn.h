@@ -150,7 +150,8 @@ int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q
 enum tmac_option {
     TMAC_OPT_SPLIT_LEN = 1,     /* group kernel: rows per workgroup; 0 = automatic (default) */
     TMAC_OPT_TARGET_GROUPS = 2, /* workgroups the automatic split aims for; 0 = one per CU */
-    TMAC_OPT_KERNEL = 3         /* a tmac_kernel_choice */
+    TMAC_OPT_KERNEL = 3,        /* a tmac_kernel_choice */
+    TMAC_OPT_ROTATE = 4         /* decode: workgroup w starts w*value steps into its rows (default 0) */
 };
 enum tmac_kernel_choice {
     TMAC_KERNEL_AUTO = 0,   /* head kernel for short contexts on few sequences, else group */

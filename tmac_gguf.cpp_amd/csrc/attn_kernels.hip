@@ -167,21 +167,31 @@ __device__ __forceinline__ void attend(const float (&q)[G][kDimsPerLane], State<
 template <int G, int KVS, int ROW, int NW, int DEPTH>
 __device__ __forceinline__ void attend_rows(const float* __restrict__ kb, const float* __restrict__ vb,
                                             int n_rows, int wave, int lane_off, int lane_row,
-                                            int lane_col, const float (&q)[G][kDimsPerLane], State<G>& st) {
+                                            int lane_col, const float (&q)[G][kDimsPerLane], State<G>& st,
+                                            int rot) {
     constexpr int PPS = kSlots / KVS;   // rows per step
     constexpr int STEP = PPS * ROW;     // floats between consecutive steps
     const int full = n_rows / PPS;      // steps whose rows are all in range
     const int nk = (full - wave + NW - 1) / NW;  // full steps of this wave: wave + NW*k
 
     if (nk > 0) {
+        // The wave visits its steps starting `rot` steps in and wrapping, so that
+        // concurrently running workgroups stream from staggered offsets of their
+        // ranges (spreads the HBM channels; the merge is order-independent).
+        rot %= nk;
         float kbuf[DEPTH][kDimsPerLane], vbuf[DEPTH][kDimsPerLane];
         const float* kp = kb + wave * STEP + lane_off;
         const float* vp = vb + wave * STEP + lane_off;
+        auto at = [&](int k) {
+            int kk = k + rot;
+            kk -= (kk >= nk) ? nk : 0;
+            return (size_t)kk * NW * STEP;
+        };
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             if (d < nk) {
-                load8(kbuf[d], kp + (size_t)d * NW * STEP);
-                load8(vbuf[d], vp + (size_t)d * NW * STEP);
+                load8(kbuf[d], kp + at(d));
+                load8(vbuf[d], vp + at(d));
             }
         }
         for (int k0 = 0; k0 < nk; k0 += DEPTH) {
@@ -191,8 +201,8 @@ __device__ __forceinline__ void attend_rows(const float* __restrict__ kb, const 
                 if (k >= nk) break;
                 attend<G, KVS, false>(q, st, kbuf[d], vbuf[d], true);
                 if (k + DEPTH < nk) {
-                    load8(kbuf[d], kp + (size_t)(k + DEPTH) * NW * STEP);
-                    load8(vbuf[d], vp + (size_t)(k + DEPTH) * NW * STEP);
+                    load8(kbuf[d], kp + at(k + DEPTH));
+                    load8(vbuf[d], vp + at(k + DEPTH));
                 }
             }
         }
@@ -362,7 +372,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     const float* kseq = a.k + base;
     const float* vseq = a.v + base;
     attend_rows<GW, KVS, ROW, NW, DEPTH>(kseq + (size_t)r0 * ROW, vseq + (size_t)r0 * ROW, max(r1 - r0, 0),
-                                         wave, lane_off, lane_row, lane_col, q, st);
+                                         wave, lane_off, lane_row, lane_col, q, st,
+                                         (blockIdx.y * gridDim.x + blockIdx.x) * a.rot_mul);
 
     if (MODE == kLayer && split == n_act - 1 && wave == 0) {
         // The new token (row `pos`): RoPE its k, write k/v to the cache row
@@ -387,6 +398,144 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     const bool direct = (n_act == 1);
     float* ws_split = direct ? nullptr : a.ws + ((size_t)seq * a.n_splits + split) * NH * kPartialStride;
     finish<GW, KVS, NW>(st, lane, wave, direct, out_heads, ws_split);
+}
+
+// Head decode for short contexts: workgroup = (query head, sequence), one
+// split, NW waves; a step is 8 rows of this head's kv head (256-byte halves of
+// the cache rows).  Everything that does not depend on the attended length --
+// the query, the new token's k/v and the first DEPTH steps of K/V (rows
+// clamped to `bound`, the rows known to be allocated) -- is loaded before the
+// length (a device-side position in layer mode) is read, so the position load
+// overlaps the K/V traffic.  Every step runs the masked path (rows at or past
+// the length get score -inf and V = 0), so the loop carries one copy of the
+// softmax state and stale rows past the length never reach the sums.
+template <int G, int KV, int NW, int DEPTH, int MODE>
+__device__ __forceinline__ void head_body(const DecodeArgs& a) {
+    constexpr int ROW = KV * kHeadDim;
+    constexpr int NH = KV * G;
+    constexpr int PPS = kSlots;      // rows per step (one kv head)
+    constexpr int STEP = PPS * ROW;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int head = blockIdx.x, seq = blockIdx.y;
+    const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
+    const int kvh = head / G;
+    const int lane_col = kvh * kHeadDim + 4 * c;
+    const int lane_off = slot * ROW + lane_col;
+
+    // 1. loads that do not depend on the length
+    float q[1][kDimsPerLane];
+    load8(q[0], a.q + ((size_t)seq * NH + head) * kHeadDim + 4 * c);
+    float kn[kDimsPerLane], vn[kDimsPerLane];
+    const bool new_lane = (MODE == kLayer) && wave == 0 && slot == 0;
+    if (new_lane) {
+        load8(kn, a.k_new + lane_col);
+        load8(vn, a.v_new + lane_col);
+    }
+    size_t base = 0;
+    int bound;  // rows that may be loaded
+    if (MODE == kUniform) {
+        base = (size_t)seq * (size_t)a.seq_stride * ROW;
+        bound = a.n_pos;
+    } else if (MODE == kRagged) {
+        base = (size_t)a.offsets[seq] * ROW;
+        bound = a.lengths[seq];
+    } else {
+        bound = a.capacity;
+    }
+    const float* kb = a.k + base + wave * STEP + lane_off;
+    const float* vb = a.v + base + wave * STEP + lane_off;
+    auto row_off = [&](int k) {  // float offset (from kb) of this lane's row in the wave's k-th step
+        const int row = (wave + NW * k) * PPS + slot;
+        const int r = min(row, bound - 1);
+        return (ptrdiff_t)(r - wave * PPS - slot) * ROW;
+    };
+    // Step 0 of every wave is loaded speculatively (rows < bound are allocated);
+    // later steps wait for the length so short contexts do not pull the whole
+    // allocation through the CU.
+    float kbuf[DEPTH][kDimsPerLane], vbuf[DEPTH][kDimsPerLane];
+    if (bound > 0) {
+        load8(kbuf[0], kb + row_off(0));
+        load8(vbuf[0], vb + row_off(0));
+    }
+
+    // 2. the attended length
+    int n_pos, pos = 0;
+    if (MODE == kLayer) {
+        pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+        if (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) {
+            if (head == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
+            return;
+        }
+        n_pos = pos + 1;
+    } else {
+        n_pos = bound;
+    }
+    float* out_head = a.out + ((size_t)seq * NH + head) * kHeadDim;
+    if (n_pos <= 0) {  // ragged sequence with no rows: defined as a zero output
+        if (threadIdx.x < kHeadDim) out_head[threadIdx.x] = 0.f;
+        return;
+    }
+    if (MODE == kRagged && n_pos > a.split_len) {  // longer than the max_len the launch was sized for
+        if (threadIdx.x < kHeadDim) out_head[threadIdx.x] = __builtin_nanf("");
+        if (threadIdx.x == 0) atomicOr(a.err, 2);
+        return;
+    }
+    const int mem_rows = (MODE == kLayer) ? pos : n_pos;
+
+    // 3. query: RoPE (layer mode) and base-2 softmax scale
+    const float2* cs_row = nullptr;
+    if (MODE == kLayer) {
+        cs_row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
+        rope8(q[0], cs_row, c);
+    }
+#pragma unroll
+    for (int t = 0; t < kDimsPerLane; ++t) q[0][t] *= a.qscale;
+
+    // 4. this wave's steps: wave + NW*k while the step starts below mem_rows
+    State<1> st;
+    state_init(st);
+    const int n_steps = (mem_rows + PPS - 1) / PPS;
+    const int nk = (n_steps - wave + NW - 1) / NW;
+#pragma unroll
+    for (int d = 1; d < DEPTH; ++d) {
+        if (d < nk) {
+            load8(kbuf[d], kb + row_off(d));
+            load8(vbuf[d], vb + row_off(d));
+        }
+    }
+    for (int k0 = 0; k0 < nk; k0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int k = k0 + d;
+            if (k >= nk) break;
+            const bool valid = (wave + NW * k) * PPS + slot < mem_rows;
+#pragma unroll
+            for (int t = 0; t < kDimsPerLane; ++t) vbuf[d][t] = valid ? vbuf[d][t] : 0.f;
+            attend<1, 1, true>(q, st, kbuf[d], vbuf[d], valid);
+            if (k + DEPTH < nk) {
+                load8(kbuf[d], kb + row_off(k + DEPTH));
+                load8(vbuf[d], vb + row_off(k + DEPTH));
+            }
+        }
+    }
+
+    // 5. layer mode: the new token (row pos) from registers; its group's first
+    //    head writes the rotated k and v to the cache row (tmac_gguf.cpp:1090-1091).
+    if (MODE == kLayer && wave == 0) {
+        if (new_lane) {
+            rope8(kn, cs_row, c);
+            if (head % G == 0) {
+                store8(a.k_out + (size_t)pos * ROW + lane_col, kn);
+                store8(a.v_out + (size_t)pos * ROW + lane_col, vn);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < kDimsPerLane; ++t) kn[t] = vn[t] = 0.f;
+        }
+        attend<1, 1, true>(q, st, kn, vn, new_lane);
+    }
+    finish<1, 1, NW>(st, lane, wave, true, out_head, nullptr);
 }
 
 // Log-sum-exp merge of the split partials: one wave per (head, sequence) with
@@ -448,7 +597,7 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(kHeadWaves * 64) void tmac_##M##_head_g##G##_kv##KV(    \
         DecodeArgs a) {                                                                            \
-        decode_body<G, KV, kHeadWaves, kHeadPrefetchDepth, MODE, true>(a);                         \
+        head_body<G, KV, kHeadWaves, kHeadPrefetchDepth, MODE>(a);                                 \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(64) void tmac_##M##_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, MODE>(a);                                                              \

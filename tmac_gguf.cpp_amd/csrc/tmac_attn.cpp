@@ -77,6 +77,7 @@ struct tmac_context {
     int64_t opt_split_len = 0;
     int64_t opt_target_groups = 0;
     int64_t opt_kernel = TMAC_KERNEL_AUTO;
+    int64_t opt_rot_mul = 0;
     std::string last_error;
     char device_name[256] = {0};
 };
@@ -261,6 +262,7 @@ const float kQScale = (float)(1.4426950408889634 / 8.0);  // log2(e) / sqrt(64)
 int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeArgs& a, int n_seq,
                int grid_rows, int n_kv_head) {
     a.qscale = kQScale;
+    a.rot_mul = (int)ctx->opt_rot_mul;
     a.err = ctx->err;
     if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
     if (use_head_kernel(ctx, n_seq, a.n_head, grid_rows)) {
@@ -602,6 +604,10 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
     switch (option) {
         case TMAC_OPT_SPLIT_LEN: ctx->opt_split_len = value; return TMAC_OK;
         case TMAC_OPT_TARGET_GROUPS: ctx->opt_target_groups = value; return TMAC_OK;
+        case TMAC_OPT_ROTATE:
+            if (value > 1 << 20) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: rotate too large");
+            ctx->opt_rot_mul = value;
+            return TMAC_OK;
         case TMAC_OPT_KERNEL:
             if (value > TMAC_KERNEL_HEAD) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: bad kernel choice");
             ctx->opt_kernel = value;

@@ -35,6 +35,7 @@ TMAC_ERR_HIP_BASE = 1000
 TMAC_OPT_SPLIT_LEN = 1
 TMAC_OPT_TARGET_GROUPS = 2
 TMAC_OPT_KERNEL = 3
+TMAC_OPT_ROTATE = 4
 TMAC_KERNEL_AUTO = 0
 TMAC_KERNEL_GROUP = 1
 TMAC_KERNEL_HEAD = 2
