@@ -217,7 +217,8 @@ def bench_c4(ctx, stream, steps, warmup, n_seq=16, max_len=32768):
     dout = ctx.empty((n_seq, NH * HD))
 
     def launch():
-        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, n_seq, NH, NKV, HD, max_len, stream=stream)
+        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, n_seq, NH, NKV, HD, max_len, total_rows=total,
+                          stream=stream)
 
     per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
     nbytes = algo_bytes(lens)
@@ -311,6 +312,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--only-c3", action="store_true", help="time config 3 only (for profiling)")
     ap.add_argument("--rotate", type=int, default=None, help="override TMAC_OPT_ROTATE (tuning)")
+    ap.add_argument("--split-len", type=int, default=None, help="override TMAC_OPT_SPLIT_LEN (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
     ap.add_argument("--sections", default="c1,c2,c4,c5",
@@ -327,6 +329,8 @@ def main():
     stream = ctx.stream()
     if args.rotate is not None:
         ctx.set_option(tmac_attn.TMAC_OPT_ROTATE, args.rotate)
+    if args.split_len is not None:
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, args.split_len)
 
     if args.copy_calib:
         n = 256 << 20

@@ -127,12 +127,14 @@ int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const f
                                   int64_t seq_stride);
 /* Ragged split-KV decode over a packed pool: sequence s attends rows
  * [offsets[s], offsets[s] + lengths[s]) (DEVICE arrays).  max_len bounds every
- * length (it sizes the grid); longer sequences are an error the caller must
- * avoid.  A sequence of length 0 produces a zero output. */
+ * length (it sizes the grid); a longer sequence gets a NaN output and raises
+ * bit 1 of the device error word.  A sequence of length 0 produces a zero
+ * output.  total_rows, if the caller knows it (sum of lengths; 0 = unknown),
+ * only tunes the split length for load balance -- results do not depend on it. */
 int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const float* q,
                                  const float* k_pool, const float* v_pool, const int64_t* offsets,
                                  const int32_t* lengths, float* out, int n_seq, int n_head,
-                                 int n_kv_head, int head_dim, int max_len);
+                                 int n_kv_head, int head_dim, int max_len, int64_t total_rows);
 
 /* ---- chunked causal prefill (extension; the reference feeds prompts one token at a time,
  *      tmac_gguf.cpp:1621-1658, so its oracle is attention_op per query row) ----

@@ -40,7 +40,7 @@ def test_calls_without_context_are_rejected():
     assert lib.tmac_elem_op(None, None, 2, 16, 16, 128) == nc
     assert lib.tmac_layer_attention(None, None, 16, 16, 16, 16, 16, 16, 14, 2, 64, 0, 256, 1e6) == nc
     assert lib.tmac_attention_decode_batched(None, None, 16, 16, 16, 16, 1, 14, 2, 64, 1, 1) == nc
-    assert lib.tmac_attention_decode_ragged(None, None, 16, 16, 16, 16, 16, 16, 1, 14, 2, 64, 1) == nc
+    assert lib.tmac_attention_decode_ragged(None, None, 16, 16, 16, 16, 16, 16, 1, 14, 2, 64, 1, 0) == nc
     assert lib.tmac_step_begin(None, None) == nc
     assert lib.tmac_malloc(None, ctypes.byref(ctypes.c_void_p()), 16) == nc
     assert lib.tmac_shutdown(None) == nc

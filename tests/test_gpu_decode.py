@@ -130,8 +130,10 @@ def test_decode_ragged(ctx, kernel):
     dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     doff, dlen = ctx.upload(offs), ctx.upload(lens)
     dout = ctx.empty((lens.size, NH * HD))
-    ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, lens.size, NH, NKV, HD, int(lens.max()))
-    assert_close(dout.numpy(), ref, f"ragged kernel={kernel}")
+    for hint in (0, total):  # the split hint changes the schedule, never the result
+        dout.fill_bytes(0xFF)
+        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, lens.size, NH, NKV, HD, int(lens.max()), total_rows=hint)
+        assert_close(dout.numpy(), ref, f"ragged kernel={kernel} total_rows hint={hint}")
     assert ctx.check_device_error() == 0
 
 

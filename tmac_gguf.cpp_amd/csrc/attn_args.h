@@ -28,6 +28,7 @@ struct DecodeArgs {
     int64_t seq_stride;      // uniform mode: rows between consecutive sequences
     int n_pos;               // uniform mode: rows attended per sequence (past_len + 1)
     int n_head;
+    int n_seq;               // ragged mode: sequences (lengths[] entries)
     int split_len;           // rows per workgroup (multiple of the group's step)
     int n_splits;            // gridDim.x
     float* ws;               // split partials [n_seq][n_splits][n_head][66] (n_splits > 1)

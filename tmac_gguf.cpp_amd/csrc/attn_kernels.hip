@@ -303,6 +303,43 @@ __device__ __forceinline__ bool seq_geometry(const DecodeArgs& a, int seq, int& 
     return true;
 }
 
+// Ragged group kernel: flat unit index -> (sequence, split).  Sequence s owns
+// clamp(ceil(L_s / split_len), 1, n_splits) consecutive units (a length above
+// the launch's max_len still gets its units, whose first one reports it), so
+// the unit count never exceeds the n_seq * n_splits grid; the units that carry
+// rows fill the front of the grid (round-robin dispatch then spreads them
+// evenly over the XCDs) and surplus workgroups at the end exit.  Every wave
+// computes the same answer with a 64-lane inclusive scan per 64 sequences.
+__device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths, int n_seq, int split_len,
+                                            int n_splits, int unit, int& seq, int& split) {
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    for (int c0 = 0; c0 < n_seq; c0 += 64) {
+        const int sq = c0 + lane;
+        int u = 0;
+        if (sq < n_seq) {
+            const int len = lengths[sq];
+            u = len > 0 ? min((len + split_len - 1) / split_len, n_splits) : 1;
+        }
+        int incl = u;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(incl, off);
+            if (lane >= off) incl += t;
+        }
+        const int total = __shfl(incl, 63);
+        if (unit < base + total) {
+            const unsigned long long hit = __ballot(unit < base + incl);
+            const int first = __ffsll((long long)hit) - 1;
+            seq = __builtin_amdgcn_readfirstlane(c0 + first);
+            split = __builtin_amdgcn_readfirstlane(unit - base - __shfl(incl - u, first));
+            return true;
+        }
+        base += total;
+    }
+    return false;
+}
+
 // Decode for one (split, sequence) workgroup.
 //   PER_HEAD = false ("group" kernel): grid (split, seq); every lane carries
 //     the G query heads of its kv head and a step covers all KV kv heads of
@@ -318,9 +355,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     constexpr int GW = PER_HEAD ? 1 : G;    // query heads per lane
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int split = PER_HEAD ? 0 : blockIdx.x;
+    int split = PER_HEAD ? 0 : blockIdx.x;
     const int head = PER_HEAD ? blockIdx.x : 0;
-    const int seq = blockIdx.y;
+    int seq = blockIdx.y;
+    if (MODE == kRagged && !PER_HEAD) {  // grid = flat list of (sequence, split) units
+        if (!ragged_unit(a.lengths, a.n_seq, a.split_len, a.n_splits, blockIdx.x, seq, split)) return;
+    }
 
     int n_pos, pos;
     size_t base;

@@ -147,15 +147,22 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
 // workgroups (one per CU by default: a 512-thread workgroup at 2 waves per
 // SIMD fills a CU) without going below one round per workgroup, and keeps at
 // most kMaxSplits splits per sequence.
-void choose_split(const tmac_context* ctx, int n_seq, int n_pos, int n_kv_head, int* split_len, int* n_splits) {
+// With `total_rows` (ragged batches: the sum of all lengths, when the caller
+// knows it) the split length is total/target instead, so the workgroups that
+// actually have rows come close to one per CU whatever the length mix.
+void choose_split(const tmac_context* ctx, int n_seq, int n_pos, int n_kv_head, int* split_len, int* n_splits,
+                  int64_t total_rows = 0) {
     const int round = kGroupWaves * (kSlotsPerWave / n_kv_head);
     const int rounds = (n_pos + round - 1) / round;
     int len;
+    const int64_t target_groups = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : (int64_t)ctx->n_cu;
     if (ctx->opt_split_len > 0) {
         len = (int)(((ctx->opt_split_len + round - 1) / round) * round);
+    } else if (total_rows > 0 && target_groups > n_seq) {
+        const int64_t per = (total_rows + (target_groups - n_seq) - 1) / (target_groups - n_seq);
+        len = (int)std::min<int64_t>(((per + round - 1) / round) * round, (int64_t)rounds * round);
     } else {
-        const int64_t target = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : (int64_t)ctx->n_cu;
-        int64_t want = (target + n_seq - 1) / (n_seq > 0 ? n_seq : 1);
+        int64_t want = (target_groups + n_seq - 1) / (n_seq > 0 ? n_seq : 1);
         if (want < 1) want = 1;
         if (want > rounds) want = rounds;
         const int64_t per = (rounds + want - 1) / want;
@@ -260,7 +267,7 @@ const float kQScale = (float)(1.4426950408889634 / 8.0);  // log2(e) / sqrt(64)
 // Common launch of a decode-family kernel, plus the split merge when the
 // rows are spread over more than one workgroup per sequence.
 int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeArgs& a, int n_seq,
-               int grid_rows, int n_kv_head) {
+               int grid_rows, int n_kv_head, int64_t total_rows = 0) {
     a.qscale = kQScale;
     a.rot_mul = (int)ctx->opt_rot_mul;
     a.err = ctx->err;
@@ -272,7 +279,7 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
         return launch(ctx, k.head, (unsigned)a.n_head, (unsigned)n_seq, kHeadWaves * 64, stream, &a);
     }
     int split_len = 0, n_splits = 0;
-    choose_split(ctx, n_seq, grid_rows, n_kv_head, &split_len, &n_splits);
+    choose_split(ctx, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows);
     a.split_len = split_len;
     a.n_splits = n_splits;
     if (n_splits > 1) {
@@ -283,7 +290,15 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     } else {
         a.ws = nullptr;
     }
-    int rc = launch(ctx, k.group, (unsigned)n_splits, (unsigned)n_seq, kGroupWaves * 64, stream, &a);
+    a.n_seq = n_seq;
+    int rc;
+    if (a.lengths) {  // ragged: flat unit grid, n_seq * n_splits bounds the unit count
+        const int64_t units = (int64_t)n_seq * n_splits;
+        if (units > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: too many splits");
+        rc = launch(ctx, k.group, (unsigned)units, 1, kGroupWaves * 64, stream, &a);
+    } else {
+        rc = launch(ctx, k.group, (unsigned)n_splits, (unsigned)n_seq, kGroupWaves * 64, stream, &a);
+    }
     if (rc || n_splits == 1) return rc;
     return launch(ctx, k.combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
 }
@@ -446,7 +461,7 @@ int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const f
 int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const float* q,
                                  const float* k_pool, const float* v_pool, const int64_t* offsets,
                                  const int32_t* lengths, float* out, int n_seq, int n_head,
-                                 int n_kv_head, int head_dim, int max_len) {
+                                 int n_kv_head, int head_dim, int max_len, int64_t total_rows) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if (!q || !k_pool || !v_pool || !offsets || !lengths || !out)
@@ -455,7 +470,8 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
         return fail(ctx, TMAC_ERR_MISALIGNED, "decode_ragged: buffers must be 16-byte aligned");
     Kernels kern;
     if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeRagged))) return rc;
-    if (n_seq < 0 || max_len < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: need max_len >= 1");
+    if (n_seq < 0 || max_len < 1 || total_rows < 0)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: need max_len >= 1, total_rows >= 0");
     if (n_seq == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
     DecodeArgs a{};
@@ -466,7 +482,7 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
     a.offsets = offsets;
     a.lengths = lengths;
     a.n_head = n_head;
-    return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head);
+    return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head, total_rows);
 }
 
 static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, const float* k_new,

@@ -61,7 +61,7 @@ SIGNATURES = {
     "tmac_pos_update": (_i, [_vp, _vp, _vp, _i, _i]),
     "tmac_rope_prepare": (_i, [_vp, _i, _f, _i]),
     "tmac_attention_decode_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
-    "tmac_attention_decode_ragged": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "tmac_attention_decode_ragged": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
     "tmac_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_set_option": (_i, [_vp, _i, _i64]),
     "tmac_query_split": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
@@ -312,10 +312,10 @@ class Context:
         return rc
 
     def decode_ragged(self, q, k_pool, v_pool, offsets, lengths, out, n_seq, n_head, n_kv_head,
-                      head_dim, max_len, stream=None, check=True) -> int:
+                      head_dim, max_len, total_rows=0, stream=None, check=True) -> int:
         rc = self.lib.tmac_attention_decode_ragged(self.handle, stream, _p(q), _p(k_pool), _p(v_pool),
                                                    _p(offsets), _p(lengths), _p(out), n_seq, n_head,
-                                                   n_kv_head, head_dim, max_len)
+                                                   n_kv_head, head_dim, max_len, total_rows)
         if check:
             self._check(rc, "decode_ragged")
         return rc
