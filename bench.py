@@ -313,6 +313,7 @@ def main():
     ap.add_argument("--only-c3", action="store_true", help="time config 3 only (for profiling)")
     ap.add_argument("--rotate", type=int, default=None, help="override TMAC_OPT_ROTATE (tuning)")
     ap.add_argument("--split-len", type=int, default=None, help="override TMAC_OPT_SPLIT_LEN (tuning)")
+    ap.add_argument("--head-waves", type=int, default=None, help="override TMAC_OPT_HEAD_WAVES (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
     ap.add_argument("--sections", default="c1,c2,c4,c5",
@@ -331,6 +332,8 @@ def main():
         ctx.set_option(tmac_attn.TMAC_OPT_ROTATE, args.rotate)
     if args.split_len is not None:
         ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, args.split_len)
+    if args.head_waves is not None:
+        ctx.set_option(tmac_attn.TMAC_OPT_HEAD_WAVES, args.head_waves)
 
     if args.copy_calib:
         n = 256 << 20
@@ -345,7 +348,7 @@ def main():
     c3, c3_data = bench_c3(ctx, stream, args.steps, args.warmup)
     log(f"[bench] C3 {c3['gbs']:.1f} GB/s, {c3['mean_ms'] * 1e3:.1f} us/launch, split {c3['split_len']}x{c3['n_splits']}")
     extra = {}
-    sections = set() if args.only_c3 else set(x for x in args.sections.split(",") if x)
+    sections = set(x for x in args.sections.split(",") if x) if not args.only_c3 else set()
     if "c1" in sections:
         extra["c1"] = bench_c1(ctx, stream)
         log(f"[bench] C1 {extra['c1']['median_us']:.2f} us/call")

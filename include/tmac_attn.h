@@ -153,7 +153,8 @@ enum tmac_option {
     TMAC_OPT_SPLIT_LEN = 1,     /* group kernel: rows per workgroup; 0 = automatic (default) */
     TMAC_OPT_TARGET_GROUPS = 2, /* workgroups the automatic split aims for; 0 = one per CU */
     TMAC_OPT_KERNEL = 3,        /* a tmac_kernel_choice */
-    TMAC_OPT_ROTATE = 4         /* decode: workgroup w starts w*value steps into its rows (default 0) */
+    TMAC_OPT_ROTATE = 4,        /* decode: workgroup w starts w*value steps into its rows (default 0) */
+    TMAC_OPT_HEAD_WAVES = 5     /* head kernel workgroup size in waves: 4, 8 or 16 (default 8) */
 };
 enum tmac_kernel_choice {
     TMAC_KERNEL_AUTO = 0,   /* head kernel for short contexts on few sequences, else group */

@@ -639,6 +639,12 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
         DecodeArgs a) {                                                                            \
         head_body<G, KV, kHeadWaves, kHeadPrefetchDepth, MODE>(a);                                 \
     }                                                                                              \
+    extern "C" __global__ __launch_bounds__(512) void tmac_##M##_head8_g##G##_kv##KV(DecodeArgs a) { \
+        head_body<G, KV, 8, kHeadPrefetchDepth, MODE>(a);                                          \
+    }                                                                                              \
+    extern "C" __global__ __launch_bounds__(256) void tmac_##M##_head4_g##G##_kv##KV(DecodeArgs a) { \
+        head_body<G, KV, 4, kHeadPrefetchDepth, MODE>(a);                                          \
+    }                                                                                              \
     extern "C" __global__ __launch_bounds__(64) void tmac_##M##_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, MODE>(a);                                                              \
     }

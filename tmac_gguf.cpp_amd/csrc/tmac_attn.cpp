@@ -66,7 +66,9 @@ struct tmac_context {
     int n_cu = 0;
     hipModule_t module = nullptr;
     std::map<std::pair<int, int>, hipFunction_t> decode[3];   // group kernel, by mode, (G, KV)
-    std::map<std::pair<int, int>, hipFunction_t> head[3];     // head kernel, same keys
+    std::map<std::pair<int, int>, hipFunction_t> head[3];     // head kernel (16 waves), same keys
+    std::map<std::pair<int, int>, hipFunction_t> head8[3];    // head kernel, 8 waves
+    std::map<std::pair<int, int>, hipFunction_t> head4[3];    // head kernel, 4 waves
     std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr;
@@ -78,6 +80,7 @@ struct tmac_context {
     int64_t opt_target_groups = 0;
     int64_t opt_kernel = TMAC_KERNEL_AUTO;
     int64_t opt_rot_mul = 0;
+    int64_t opt_head_waves = 8;
     std::string last_error;
     char device_name[256] = {0};
 };
@@ -120,6 +123,7 @@ bool capturing(hipStream_t s) {
 
 struct Kernels {
     hipFunction_t group = nullptr, head = nullptr, combine = nullptr;
+    int head_waves = 16;
 };
 
 // Validates the attention shape shared by every decode entry point.
@@ -136,7 +140,8 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
                         std::to_string(n_kv_head));
     if (k) {
         k->group = it->second;
-        k->head = ctx->head[mode].at({g, n_kv_head});
+        k->head_waves = (int)ctx->opt_head_waves;
+        k->head = (k->head_waves == 8 ? ctx->head8 : k->head_waves == 4 ? ctx->head4 : ctx->head)[mode].at({g, n_kv_head});
         k->combine = ctx->combine[mode].at({g, n_kv_head});
     }
     return TMAC_OK;
@@ -276,7 +281,7 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
         a.split_len = grid_rows;
         a.n_splits = 1;
         a.ws = nullptr;
-        return launch(ctx, k.head, (unsigned)a.n_head, (unsigned)n_seq, kHeadWaves * 64, stream, &a);
+        return launch(ctx, k.head, (unsigned)a.n_head, (unsigned)n_seq, k.head_waves * 64, stream, &a);
     }
     int split_len = 0, n_splits = 0;
     choose_split(ctx, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows);
@@ -372,6 +377,14 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->head[m][{sh[0], sh[1]}] = f;
+            std::snprintf(name, sizeof(name), "%s_head8_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
+            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                return bail(hip_fail(ctx, e, name));
+            ctx->head8[m][{sh[0], sh[1]}] = f;
+            std::snprintf(name, sizeof(name), "%s_head4_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
+            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                return bail(hip_fail(ctx, e, name));
+            ctx->head4[m][{sh[0], sh[1]}] = f;
             std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
@@ -623,6 +636,11 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
         case TMAC_OPT_ROTATE:
             if (value > 1 << 20) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: rotate too large");
             ctx->opt_rot_mul = value;
+            return TMAC_OK;
+        case TMAC_OPT_HEAD_WAVES:
+            if (value != 4 && value != 8 && value != 16)
+                return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: head waves must be 4, 8 or 16");
+            ctx->opt_head_waves = value;
             return TMAC_OK;
         case TMAC_OPT_KERNEL:
             if (value > TMAC_KERNEL_HEAD) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: bad kernel choice");
