@@ -34,6 +34,7 @@ struct DecodeArgs {
     float* ws;               // split partials [n_seq][n_splits][n_head][66] (n_splits > 1)
     float qscale;            // log2(e) / sqrt(head_dim): softmax runs in base 2
     int rot_mul;             // workgroup w starts its step sequence w*rot_mul steps in (HBM channel spread)
+    int blocked;             // group kernel: 1 = each wave streams a contiguous run of steps
     // layer mode (RoPE + cache write + attention in one launch)
     const float* k_new;      // [n_kv_head][64] pre-RoPE
     const float* v_new;      // [n_kv_head][64]

@@ -168,11 +168,23 @@ template <int G, int KVS, int ROW, int NW, int DEPTH>
 __device__ __forceinline__ void attend_rows(const float* __restrict__ kb, const float* __restrict__ vb,
                                             int n_rows, int wave, int lane_off, int lane_row,
                                             int lane_col, const float (&q)[G][kDimsPerLane], State<G>& st,
-                                            int rot) {
+                                            int rot, bool blocked) {
     constexpr int PPS = kSlots / KVS;   // rows per step
     constexpr int STEP = PPS * ROW;     // floats between consecutive steps
     const int full = n_rows / PPS;      // steps whose rows are all in range
-    const int nk = (full - wave + NW - 1) / NW;  // full steps of this wave: wave + NW*k
+    // Interleaved: wave w takes steps w, w + NW, ...  Blocked: wave w takes a
+    // contiguous run of steps (NW independent streams per workgroup).
+    int first, nk, stride;
+    if (blocked) {
+        const int per = (full + NW - 1) / NW;
+        first = wave * per;
+        nk = max(min(full - first, per), 0);
+        stride = 1;
+    } else {
+        first = wave;
+        nk = (full - wave + NW - 1) / NW;
+        stride = NW;
+    }
 
     if (nk > 0) {
         // The wave visits its steps starting `rot` steps in and wrapping, so that
@@ -180,30 +192,30 @@ __device__ __forceinline__ void attend_rows(const float* __restrict__ kb, const 
         // ranges (spreads the HBM channels; the merge is order-independent).
         rot %= nk;
         float kbuf[DEPTH][kDimsPerLane], vbuf[DEPTH][kDimsPerLane];
-        const float* kp = kb + wave * STEP + lane_off;
-        const float* vp = vb + wave * STEP + lane_off;
+        const float* kp = kb + (size_t)first * STEP + lane_off;
+        const float* vp = vb + (size_t)first * STEP + lane_off;
         auto at = [&](int k) {
             int kk = k + rot;
             kk -= (kk >= nk) ? nk : 0;
-            return (size_t)kk * NW * STEP;
+            return (size_t)kk * stride * STEP;
         };
+        // Prefetches are unconditional (indices past the wave's last step are
+        // clamped to it, an L2 hit), so every buffer keeps one register
+        // assignment across iterations; a conditional load would make the
+        // compiler rotate buffers with copies, which must first wait for all
+        // loads in flight.
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            if (d < nk) {
-                load8(kbuf[d], kp + at(d));
-                load8(vbuf[d], vp + at(d));
-            }
+            load8(kbuf[d], kp + at(min(d, nk - 1)));
+            load8(vbuf[d], vp + at(min(d, nk - 1)));
         }
         for (int k0 = 0; k0 < nk; k0 += DEPTH) {
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
-                const int k = k0 + d;
-                if (k >= nk) break;
-                attend<G, KVS, false>(q, st, kbuf[d], vbuf[d], true);
-                if (k + DEPTH < nk) {
-                    load8(kbuf[d], kp + at(k + DEPTH));
-                    load8(vbuf[d], vp + at(k + DEPTH));
-                }
+                if (k0 + d < nk) attend<G, KVS, false>(q, st, kbuf[d], vbuf[d], true);
+                const int kn = min(k0 + d + DEPTH, nk - 1);
+                load8(kbuf[d], kp + at(kn));
+                load8(vbuf[d], vp + at(kn));
             }
         }
     }
@@ -413,7 +425,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     const float* vseq = a.v + base;
     attend_rows<GW, KVS, ROW, NW, DEPTH>(kseq + (size_t)r0 * ROW, vseq + (size_t)r0 * ROW, max(r1 - r0, 0),
                                          wave, lane_off, lane_row, lane_col, q, st,
-                                         (blockIdx.y * gridDim.x + blockIdx.x) * a.rot_mul);
+                                         (blockIdx.y * gridDim.x + blockIdx.x) * a.rot_mul, a.blocked != 0);
 
     if (MODE == kLayer && split == n_act - 1 && wave == 0) {
         // The new token (row `pos`): RoPE its k, write k/v to the cache row
@@ -634,6 +646,9 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_##M##_g##G##_kv##KV(        \
         DecodeArgs a) {                                                                            \
         decode_body<G, KV, kGroupWaves, kPrefetchDepth, MODE, false>(a);                           \
+    }                                                                                              \
+    extern "C" __global__ __launch_bounds__(256) void tmac_##M##_g4w_g##G##_kv##KV(DecodeArgs a) {  \
+        decode_body<G, KV, 4, kPrefetchDepth, MODE, false>(a);                                     \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(kHeadWaves * 64) void tmac_##M##_head_g##G##_kv##KV(    \
         DecodeArgs a) {                                                                            \

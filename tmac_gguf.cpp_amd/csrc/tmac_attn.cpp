@@ -66,6 +66,7 @@ struct tmac_context {
     int n_cu = 0;
     hipModule_t module = nullptr;
     std::map<std::pair<int, int>, hipFunction_t> decode[3];   // group kernel, by mode, (G, KV)
+    std::map<std::pair<int, int>, hipFunction_t> decode4[3];  // group kernel with 4-wave workgroups
     std::map<std::pair<int, int>, hipFunction_t> head[3];     // head kernel (16 waves), same keys
     std::map<std::pair<int, int>, hipFunction_t> head8[3];    // head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> head4[3];    // head kernel, 4 waves
@@ -81,6 +82,8 @@ struct tmac_context {
     int64_t opt_kernel = TMAC_KERNEL_AUTO;
     int64_t opt_rot_mul = 0;
     int64_t opt_head_waves = 8;
+    int64_t opt_blocked = 0;
+    int64_t opt_group_waves = 8;
     std::string last_error;
     char device_name[256] = {0};
 };
@@ -124,6 +127,7 @@ bool capturing(hipStream_t s) {
 struct Kernels {
     hipFunction_t group = nullptr, head = nullptr, combine = nullptr;
     int head_waves = 16;
+    int group_waves = 8;
 };
 
 // Validates the attention shape shared by every decode entry point.
@@ -139,7 +143,8 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
                     "no kernel for n_head/n_kv_head = " + std::to_string(g) + ", n_kv_head = " +
                         std::to_string(n_kv_head));
     if (k) {
-        k->group = it->second;
+        k->group_waves = (int)ctx->opt_group_waves;
+        k->group = k->group_waves == 4 ? ctx->decode4[mode].at({g, n_kv_head}) : it->second;
         k->head_waves = (int)ctx->opt_head_waves;
         k->head = (k->head_waves == 8 ? ctx->head8 : k->head_waves == 4 ? ctx->head4 : ctx->head)[mode].at({g, n_kv_head});
         k->combine = ctx->combine[mode].at({g, n_kv_head});
@@ -157,7 +162,7 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
 // actually have rows come close to one per CU whatever the length mix.
 void choose_split(const tmac_context* ctx, int n_seq, int n_pos, int n_kv_head, int* split_len, int* n_splits,
                   int64_t total_rows = 0) {
-    const int round = kGroupWaves * (kSlotsPerWave / n_kv_head);
+    const int round = (int)ctx->opt_group_waves * (kSlotsPerWave / n_kv_head);
     const int rounds = (n_pos + round - 1) / round;
     int len;
     const int64_t target_groups = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : (int64_t)ctx->n_cu;
@@ -275,6 +280,7 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
                int grid_rows, int n_kv_head, int64_t total_rows = 0) {
     a.qscale = kQScale;
     a.rot_mul = (int)ctx->opt_rot_mul;
+    a.blocked = (int)ctx->opt_blocked;
     a.err = ctx->err;
     if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
     if (use_head_kernel(ctx, n_seq, a.n_head, grid_rows)) {
@@ -300,9 +306,9 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     if (a.lengths) {  // ragged: flat unit grid, n_seq * n_splits bounds the unit count
         const int64_t units = (int64_t)n_seq * n_splits;
         if (units > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: too many splits");
-        rc = launch(ctx, k.group, (unsigned)units, 1, kGroupWaves * 64, stream, &a);
+        rc = launch(ctx, k.group, (unsigned)units, 1, k.group_waves * 64, stream, &a);
     } else {
-        rc = launch(ctx, k.group, (unsigned)n_splits, (unsigned)n_seq, kGroupWaves * 64, stream, &a);
+        rc = launch(ctx, k.group, (unsigned)n_splits, (unsigned)n_seq, k.group_waves * 64, stream, &a);
     }
     if (rc || n_splits == 1) return rc;
     return launch(ctx, k.combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
@@ -373,6 +379,10 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->decode[m][{sh[0], sh[1]}] = f;
+            std::snprintf(name, sizeof(name), "%s_g4w_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
+            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                return bail(hip_fail(ctx, e, name));
+            ctx->decode4[m][{sh[0], sh[1]}] = f;
             std::snprintf(name, sizeof(name), "%s_head_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
@@ -636,6 +646,14 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
         case TMAC_OPT_ROTATE:
             if (value > 1 << 20) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: rotate too large");
             ctx->opt_rot_mul = value;
+            return TMAC_OK;
+        case TMAC_OPT_WAVE_ORDER:
+            if (value > 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: wave order is 0 or 1");
+            ctx->opt_blocked = value;
+            return TMAC_OK;
+        case TMAC_OPT_GROUP_WAVES:
+            if (value != 4 && value != 8) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: group waves must be 4 or 8");
+            ctx->opt_group_waves = value;
             return TMAC_OK;
         case TMAC_OPT_HEAD_WAVES:
             if (value != 4 && value != 8 && value != 16)
