@@ -58,11 +58,17 @@ struct PrefillArgs {
     int64_t seq_stride;
     int n_q;
     int prefix_len;
+    int n_qblk;              // ceil(n_q / kPrefillQueries); attention grid = n_qblk * n_kv_head * n_seq
     float qscale;            // log2(e) / sqrt(head_dim)
+    uint16_t* packed;        // bf16 tiles [n_seq][n_kv_head][n_tp][K tile, V^T tile] (64 x 64 each)
+    int n_tp;                // tiles per (sequence, kv head): ceil(n_rows / 64) rounded up to a stage
+    int n_rows;              // prefix_len + n_q: cache rows that are packed
 };
 constexpr int kPrefillQueries = 16;  // queries per workgroup (one MFMA column block)
-constexpr int kPrefillKeys = 64;     // keys per LDS tile
-constexpr int kPrefillWaves = 8;     // waves per workgroup (G <= 8 compute, all load)
+constexpr int kPrefillKeys = 64;     // keys per tile
+constexpr int kPrefillTileElems = 2 * 64 * 64;  // bf16 per packed tile: K [key][dim], then V^T [dim][key]
+constexpr int kPrefillStageTiles = 4;           // tiles per LDS stage (two per wave and head pair)
+constexpr int kPrefillWaves = 8;     // waves per workgroup: 4 head pairs x 2 stage halves
 
 struct RopeArgs {
     float* x;                // [n_heads][64], rotated in place

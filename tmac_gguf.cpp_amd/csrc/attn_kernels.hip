@@ -681,176 +681,389 @@ TMAC_DECODE_KERNELS(8, 1)
 // ---------------------------------------------------------------------------
 // Chunked causal prefill on bf16 MFMA (v_mfma_f32_16x16x32_bf16).
 //
-// Workgroup = (16-query block, kv head, sequence), 8 waves; wave w < G owns
-// query head kv*G + w.  Per 64-key tile all 512 lanes load K and V (fp32) for
-// the kv head, convert to bf16 (round to nearest even) and stage K as
-// [key][dim] and V as V^T [dim][key] in LDS (rows padded to 72 bf16), shared
-// by the G heads of the group.  Each compute wave works transposed:
-//   S^T (64 keys x 16 queries) = K (keys x dims) . Q^T        8 MFMAs
-//   O^T (64 dims x 16 queries) += V^T (dims x keys) . P^T    16 MFMAs
-// so lane l owns query column l%16 in every accumulator and the online
-// softmax (max, rescale, row sum) is lane-local except for two xor shuffles
-// per tile.  P is split into bf16 hi + lo parts (two PV MFMAs), which keeps
-// the weights to ~2^-17 relative error; with bf16-representable q/k/v the
-// result matches an fp32 evaluation to fp32 rounding.  The key order inside
-// each PV K-step is a permutation shared by the V^T and P^T operands, which
-// leaves the contraction unchanged.
+// Two launches.  The pack kernel rounds the cache rows 0 .. prefix + n_q - 1
+// of every (sequence, kv head) to bf16 (nearest even) once, into 64-key tiles
+// laid out exactly as the attention kernel keeps them in LDS: K as
+// [key][dim], V^T as [dim][key'], 64 x 64 each, 16-byte chunks XOR-swizzled
+// per row.  The attention kernel then moves tiles into LDS with direct
+// global-to-LDS loads (no registers, no conversion), four tiles per stage,
+// double-buffered, one barrier per stage.
+//
+// Attention workgroup = (16-query block, kv head, sequence), 8 waves.  The
+// 1-D grid is ordered so that the blocks of one (sequence, kv head) run on the
+// same XCD (workgroups are dealt to the 8 XCDs round-robin) and share its L2
+// copy of that head's tiles; within an XCD the longest query blocks start
+// first.  Wave w computes tiles 2 * (w / 4) and 2 * (w / 4) + 1 of every stage
+// for the query heads 2p and 2p + 1 of the group (p = w % 4; a missing second
+// head repeats the first and is not stored), so every K and V^T operand read
+// from LDS feeds two heads' MFMAs.  Each wave works transposed,
+//   S^T (64 keys x 16 queries) = K (keys x dims) . Q^T         8 MFMAs / head / tile
+//   O^T (64 dims x 16 queries) += V^T (dims x keys) . P^T     16 MFMAs / head / tile
+// so lane l owns query column l % 16 in every accumulator and the online
+// softmax is lane-local except for two lane swaps per tile pair.  The running
+// max is only raised when a tile pair exceeds it by more than 2^kTau (a rare,
+// wave-uniform branch).  P is split into bf16 hi (truncated) + lo (rounded)
+// parts, two PV MFMAs, which keeps the weights to ~2^-16 relative error; with
+// bf16-representable q/k/v the result matches an fp32 evaluation to fp32
+// rounding.  The two tile halves of a head are merged through LDS at the end.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
-constexpr int kTileStride = 72;  // bf16 per LDS row (64 + 8 pad: conflict-free 16-byte reads)
+constexpr int kStageElems = kPrefillStageTiles * kPrefillTileElems;  // bf16 per LDS stage buffer (64 KiB)
+
+// Column of key `key` (0..63) in a V^T row.  Inside each 32-key half the
+// S^T accumulator hands lane group g4 the keys 4*g4 + i and 16 + 4*g4 + i
+// (i < 4); this order puts those 8 keys side by side, so the V^T operand of a
+// PV MFMA is one 16-byte read.  The P^T operand uses the same key order.
+__device__ __forceinline__ int vt_col(int key) {
+    const int k = key & 31;
+    return (key & 32) + 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3);
+}
+// Inverse of vt_col: the key stored at V^T column p.
+__device__ __forceinline__ int vt_key(int p) {
+    const int q = p & 31;
+    return (p & 32) + 16 * ((q >> 2) & 1) + 4 * (q >> 3) + (q & 3);
+}
+
+// Element offset of (row, column) in a 64 x 64 bf16 tile: the 16-byte chunk
+// c / 8 of row r is stored at chunk (c / 8) ^ sw(r), sw(r) = (r ^ r / 8) % 8.
+// An MFMA operand read (16 consecutive rows, one chunk each) then touches 16
+// distinct (row parity, chunk) bank groups.
+__device__ __forceinline__ int tile_offset(int r, int c) {
+    const int sw = (r ^ (r >> 3)) & 7;
+    return r * 64 + ((((c >> 3) ^ sw)) << 3) + (c & 7);
+}
+
+__device__ __forceinline__ unsigned bf16_pair(float a, float b) {
+    const bf16x2 v = {(__bf16)a, (__bf16)b};  // round to nearest even
+    return __builtin_bit_cast(unsigned, v);
+}
+
+// Max / sum over the four lanes l % 16 + 16 * k (k = 0..3) of a wave, via the
+// gfx950 row and half-wave swaps (each returns both swapped registers; the
+// reduction of the pair is the same whichever way round they come).
+__device__ __forceinline__ float max4_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum4_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Pack one 64-row tile of one (sequence, kv head): 256 threads, thread t owns
+// row t / 4 and columns 16 * (t % 4) .. + 15 of the K tile and of the V^T tile.
+// Rows at or past n_rows are written as zeros.
+template <int KV>
+__device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
+    constexpr int ROW = KV * kHeadDim;
+    const int tile = blockIdx.x % a.n_tp;
+    const int rest = blockIdx.x / a.n_tp;
+    const int kv = rest % KV, seq = rest / KV;
+    const int tid = threadIdx.x, r = tid >> 2, q4 = tid & 3;
+    const int key = tile * kPrefillKeys + r;
+    const size_t row = (size_t)seq * a.seq_stride + (size_t)min(key, a.n_rows - 1);
+    const float* kp = a.k + row * ROW + kv * kHeadDim + 16 * q4;
+    const float* vp = a.v + row * ROW + kv * kHeadDim + 16 * q4;
+    const bool valid = key < a.n_rows;
+    __shared__ float sv[64][65];
+    float kx[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 kf = *reinterpret_cast<const float4*>(kp + 4 * i);
+        const float4 vf = *reinterpret_cast<const float4*>(vp + 4 * i);
+        kx[4 * i + 0] = valid ? kf.x : 0.f;
+        kx[4 * i + 1] = valid ? kf.y : 0.f;
+        kx[4 * i + 2] = valid ? kf.z : 0.f;
+        kx[4 * i + 3] = valid ? kf.w : 0.f;
+        sv[r][16 * q4 + 4 * i + 0] = valid ? vf.x : 0.f;
+        sv[r][16 * q4 + 4 * i + 1] = valid ? vf.y : 0.f;
+        sv[r][16 * q4 + 4 * i + 2] = valid ? vf.z : 0.f;
+        sv[r][16 * q4 + 4 * i + 3] = valid ? vf.w : 0.f;
+    }
+    __bf16* dst = reinterpret_cast<__bf16*>(a.packed) +
+                  (((size_t)seq * KV + kv) * a.n_tp + tile) * kPrefillTileElems;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+        const float* x = kx + 8 * cc;
+        const u32x4 w = {bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3]), bf16_pair(x[4], x[5]),
+                         bf16_pair(x[6], x[7])};
+        *reinterpret_cast<u32x4*>(dst + tile_offset(r, 16 * q4 + 8 * cc)) = w;
+    }
+    __syncthreads();
+    // V^T row d = r, columns p = 16 * q4 .. + 15 hold keys vt_key(p)
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = sv[vt_key(16 * q4 + 8 * cc + e)][r];
+        const u32x4 w = {bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3]), bf16_pair(x[4], x[5]),
+                         bf16_pair(x[6], x[7])};
+        *reinterpret_cast<u32x4*>(dst + 64 * 64 + tile_offset(r, 16 * q4 + 8 * cc)) = w;
+    }
+}
 
 template <int G, int KV>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
-    constexpr int ROW = KV * kHeadDim;
     constexpr int NH = KV * G;
-    constexpr int QB = kPrefillQueries, KT = kPrefillKeys;
-    static_assert(G <= kPrefillWaves, "one compute wave per query head of the group");
+    constexpr int QB = kPrefillQueries, KT = kPrefillKeys, NT = kPrefillStageTiles;
+    static_assert(G <= 2 * 4, "four head pairs per workgroup");
+    static_assert(kPrefillWaves == 2 * NT, "one wave per (head pair, half stage)");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int qblk = blockIdx.x, kv = blockIdx.y, seq = blockIdx.z;
+    const int pair = wave & 3, part = wave >> 2;  // head pair, half of the stage (two tiles)
+
+    // XCD-aware block order: XCD x (= blockIdx.x % 8) owns a contiguous run of
+    // the logical block range.
+    const int n_blk = gridDim.x, xcd = blockIdx.x & 7;
+    const int per = n_blk >> 3, rem = n_blk & 7;
+    const int logical = xcd * per + min(xcd, rem) + (blockIdx.x >> 3);
+    const int sk = logical / a.n_qblk;                  // (sequence, kv head)
+    const int qblk = a.n_qblk - 1 - (logical - sk * a.n_qblk);
+    const int seq = sk / KV, kv = sk - seq * KV;
     const int q0 = qblk * QB;
-    if (q0 >= a.n_q) return;
     const int q_last = min(q0 + QB, a.n_q) - 1;
-    const int kmax = a.prefix_len + q_last;          // last key any query of the block attends
+    const int kmax = a.prefix_len + q_last;  // last key any query of the block attends
     const int n_tiles = kmax / KT + 1;
-    const float* kseq = a.k + (size_t)seq * a.seq_stride * ROW + kv * kHeadDim;
-    const float* vseq = a.v + (size_t)seq * a.seq_stride * ROW + kv * kHeadDim;
+    const int n_stages = (n_tiles + NT - 1) / NT;
+    const __bf16* slab = reinterpret_cast<const __bf16*>(a.packed) + (size_t)sk * a.n_tp * kPrefillTileElems;
 
-    __shared__ __bf16 s_k[KT * kTileStride];   // [key][dim]
-    __shared__ __bf16 s_vt[kHeadDim * kTileStride];  // [dim][key]
+    // Two stage buffers as separate objects, so that the compiler sees that a
+    // direct load into one does not alias the operand reads from the other.
+    __shared__ __attribute__((aligned(16))) __bf16 buf0[kStageElems];
+    __shared__ __attribute__((aligned(16))) __bf16 buf1[kStageElems];
 
-    const int col = lane & 15;   // query column / MFMA row index
-    const int g4 = lane >> 4;    // k-group of the MFMA operands
-    const bool compute = wave < G;
-    const int head = kv * G + (compute ? wave : 0);
+    const int col = lane & 15;  // query column / MFMA row index
+    const int g4 = lane >> 4;   // k-group of the MFMA operands
+    const bool compute = 2 * pair < G;
+    const int hl[2] = {min(2 * pair, G - 1), min(2 * pair + 1, G - 1)};
     const int qi = q0 + col;
     const int ap = a.prefix_len + qi;  // absolute position of this lane's query
+    const float c = a.qscale;
 
-    // Q^T operand: this lane's query, dims 32j + 8*g4 + (0..7), j = 0, 1.
-    bf16x8 qop[2];
-    {
-        const float* qp = a.q + (((size_t)seq * a.n_q + min(qi, a.n_q - 1)) * NH + head) * kHeadDim;
+    // Q^T operands: this lane's query, dims 32j + 8*g4 + (0..7).
+    bf16x8 qop[2][2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const float* qp = a.q + (((size_t)seq * a.n_q + min(qi, a.n_q - 1)) * NH + kv * G + hl[hh]) * kHeadDim;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * j + 8 * g4);
             const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * j + 8 * g4 + 4);
-            qop[j][0] = (__bf16)x0.x; qop[j][1] = (__bf16)x0.y; qop[j][2] = (__bf16)x0.z; qop[j][3] = (__bf16)x0.w;
-            qop[j][4] = (__bf16)x1.x; qop[j][5] = (__bf16)x1.y; qop[j][6] = (__bf16)x1.z; qop[j][7] = (__bf16)x1.w;
+            const u32x4 w = {bf16_pair(x0.x, x0.y), bf16_pair(x0.z, x0.w), bf16_pair(x1.x, x1.y),
+                             bf16_pair(x1.z, x1.w)};
+            qop[hh][j] = __builtin_bit_cast(bf16x8, w);
         }
     }
-
-    f32x4 o[4];  // O^T blocks: dims 16*db + 4*g4 + i, query col
+    // per-lane operand offsets inside a K or V^T tile: rows 16 b + col, chunk 4 j + g4
+    int op_off[4][2];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m = kNegInf, lsum = 0.f;
-
-    // Tile loaders: K as 2 float4 per thread, V as a key pair x float4.
-    const int kf0 = tid, kf1 = tid + 512;  // float4 index = key * 16 + col4
-    const int vpair = tid >> 4, vcol4 = tid & 15;
-    float4 kr0, kr1, vr0, vr1;
-    auto load_tile = [&](int t) {
-        const int base = t * KT;
-        const int k0 = min(base + (kf0 >> 4), kmax), k1 = min(base + (kf1 >> 4), kmax);
-        kr0 = *reinterpret_cast<const float4*>(kseq + (size_t)k0 * ROW + 4 * (kf0 & 15));
-        kr1 = *reinterpret_cast<const float4*>(kseq + (size_t)k1 * ROW + 4 * (kf1 & 15));
-        const int v0 = min(base + 2 * vpair, kmax), v1 = min(base + 2 * vpair + 1, kmax);
-        vr0 = *reinterpret_cast<const float4*>(vseq + (size_t)v0 * ROW + 4 * vcol4);
-        vr1 = *reinterpret_cast<const float4*>(vseq + (size_t)v1 * ROW + 4 * vcol4);
-    };
-    auto store_tile = [&]() {
-        bf16x4 k0v = {(__bf16)kr0.x, (__bf16)kr0.y, (__bf16)kr0.z, (__bf16)kr0.w};
-        bf16x4 k1v = {(__bf16)kr1.x, (__bf16)kr1.y, (__bf16)kr1.z, (__bf16)kr1.w};
-        *reinterpret_cast<bf16x4*>(&s_k[(kf0 >> 4) * kTileStride + 4 * (kf0 & 15)]) = k0v;
-        *reinterpret_cast<bf16x4*>(&s_k[(kf1 >> 4) * kTileStride + 4 * (kf1 & 15)]) = k1v;
-        const float a0[4] = {vr0.x, vr0.y, vr0.z, vr0.w}, a1[4] = {vr1.x, vr1.y, vr1.z, vr1.w};
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-            bf16x2 pr = {(__bf16)a0[i], (__bf16)a1[i]};
-            *reinterpret_cast<bf16x2*>(&s_vt[(4 * vcol4 + i) * kTileStride + 2 * vpair]) = pr;
-        }
+        for (int j = 0; j < 2; ++j) op_off[b][j] = tile_offset(16 * b + col, 32 * j + 8 * g4);
+
+    // O^T blocks 0..3: dims 16*db + 4*g4 + i for query col.  Block 4 is the
+    // softmax row sum: its A operand is a constant row of ones (row 0 of the
+    // block), so O^T[4] row 0 = sum over keys of P, accumulated from the same
+    // bf16 hi/lo weights as the output.
+    f32x4 o[2][5];
+    float m[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        m[hh] = kNegInf;
+#pragma unroll
+        for (int db = 0; db < 5; ++db) o[hh][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    bf16x8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (__bf16)(col == 0 ? 1.f : 0.f);
+
+    // Direct loads of stage st (NT tiles, contiguous in the slab): each wave
+    // moves kPieces KiB; lane l's 16 bytes land at piece + 16 l.
+    constexpr int kPieces = kStageElems / 512 / kPrefillWaves;
+    auto dma = [&](int st, __bf16* dst) {
+        const __bf16* src = slab + (size_t)st * kStageElems + (wave * kPieces) * 512 + lane * 8;
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i)
+            __builtin_amdgcn_global_load_lds(src + i * 512, (lds_void_ptr)(dst + (wave * kPieces + i) * 512), 16,
+                                             0, 0);
     };
 
-    load_tile(0);
-    for (int t = 0; t < n_tiles; ++t) {
-        __syncthreads();  // previous tile's LDS reads are done
-        store_tile();
-        __syncthreads();
-        if (t + 1 < n_tiles) load_tile(t + 1);  // in flight during this tile's MFMAs
-        if (compute) {
-            // S^T = K . Q^T
-            f32x4 st[4];
+    // Two consecutive tiles (keys kbase .. kbase + 127) for the wave's two
+    // heads; `diag` (wave-uniform) applies the causal mask.
+    auto tile_pair = [&](const __bf16* tb, int kbase, bool diag) {
+        f32x4 sc[2][2][4];  // [tile][head][key block]
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const __bf16* tk = tb + u * kPrefillTileElems;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-                st[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                sc[u][0][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                sc[u][1][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(
-                        &s_k[(16 * kb + col) * kTileStride + 32 * j + 8 * g4]);
-                    st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[j], st[kb], 0, 0, 0);
-                }
-            }
-            // scale, causal mask, online softmax for query `col`
-            const int kbase = t * KT;
-            const bool diag = kbase + KT - 1 > a.prefix_len + q0;  // tile reaches past some query
-            float tmax = kNegInf;
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float sv = st[kb][i] * a.qscale;
-                    if (diag && kbase + 16 * kb + 4 * g4 + i > ap) sv = kNegInf;
-                    st[kb][i] = sv;
-                    tmax = fmaxf(tmax, sv);
-                }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float mn = fmaxf(m, tmax);
-            const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
-            m = mn;
-            lsum *= alpha;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) o[db] *= alpha;
-            // P^T operands (hi, lo) for the two PV K-steps: keys 32j + 4*g4 + i, 32j + 16 + 4*g4 + i
-            bf16x8 ph[2], pl[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float p = fast_exp2(st[2 * j + h][i] - mn);
-                        lsum += p;
-                        const __bf16 hi = (__bf16)p;
-                        ph[j][4 * h + i] = hi;
-                        pl[j][4 * h + i] = (__bf16)(p - (float)hi);
-                    }
-            // O^T += V^T . P^T
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const __bf16* vrow = &s_vt[(16 * db + col) * kTileStride + 32 * j + 4 * g4];
-                    const bf16x4 va = *reinterpret_cast<const bf16x4*>(vrow);
-                    const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vrow + 16);
-                    const bf16x8 vop = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
-                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, ph[j], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pl[j], o[db], 0, 0, 0);
+                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tk + op_off[kb][j]);
+                    sc[u][0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[0][j], sc[u][0][kb], 0, 0, 0);
+                    sc[u][1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[1][j], sc[u][1][kb], 0, 0, 0);
                 }
             }
         }
-    }
-    if (!compute || qi >= a.n_q) return;
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    const float inv = 1.f / lsum;
-    float* op = a.out + (((size_t)seq * a.n_q + qi) * NH + head) * kHeadDim + 4 * g4;
+        if (diag) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-        *reinterpret_cast<float4*>(op + 16 * db) =
-            make_float4(o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv);
+            for (int u = 0; u < 2; ++u) {
+                const int lim = ap - kbase - KT * u - 4 * g4;  // key 16 kb + i of tile u is visible iff <= lim
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (16 * kb + i > lim) sc[u][hh][kb][i] = kNegInf;
+            }
+        }
+        float tm[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            tm[hh] = kNegInf;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) tm[hh] = fmaxf(tm[hh], sc[u][hh][kb][i]);
+            tm[hh] = max4_rows(tm[hh]);
+        }
+        // raise a running max only when the pair exceeds it by > 2^kTau (rare, wave-uniform)
+        if (__any((tm[0] - m[0]) * c > kTau || (tm[1] - m[1]) * c > kTau)) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const float mn = fmaxf(m[hh], tm[hh]);
+                const float alpha = (m[hh] == kNegInf) ? 0.f : fast_exp2((m[hh] - mn) * c);
+                m[hh] = mn;
+#pragma unroll
+                for (int db = 0; db < 5; ++db) o[hh][db] *= alpha;
+            }
+        }
+        const float mc[2] = {(m[0] == kNegInf) ? 0.f : m[0] * c, (m[1] == kNegInf) ? 0.f : m[1] * c};
+        // P^T (hi, lo) and O^T += V^T . P^T; one basic block, so exponentials
+        // of one (tile, head) can issue under the MFMAs of the previous one.
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const __bf16* tv = tb + u * kPrefillTileElems + 64 * 64;
+            bf16x8 va[4][2];
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) va[db][j] = *reinterpret_cast<const bf16x8*>(tv + op_off[db][j]);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                // P^T operands for PV K-step j: keys 32j + 16h + 4*g4 + i  <->  S^T block 2j + h, row i
+                u32x4 ph[2], pl[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int i = 0; i < 4; i += 2) {
+                            const float p0 = fast_exp2(__builtin_fmaf(sc[u][hh][2 * j + h][i], c, -mc[hh]));
+                            const float p1 = fast_exp2(__builtin_fmaf(sc[u][hh][2 * j + h][i + 1], c, -mc[hh]));
+                            const unsigned u0 = __float_as_uint(p0) & 0xffff0000u;
+                            const unsigned u1 = __float_as_uint(p1) & 0xffff0000u;
+                            ph[j][2 * h + i / 2] = (u0 >> 16) | u1;
+                            pl[j][2 * h + i / 2] =
+                                bf16_pair(p0 - __uint_as_float(u0), p1 - __uint_as_float(u1));
+                        }
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        o[hh][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            va[db][j], __builtin_bit_cast(bf16x8, ph[j]), o[hh][db], 0, 0, 0);
+                        o[hh][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            va[db][j], __builtin_bit_cast(bf16x8, pl[j]), o[hh][db], 0, 0, 0);
+                    }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    o[hh][4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(bf16x8, ph[j]),
+                                                                       o[hh][4], 0, 0, 0);
+                    o[hh][4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(bf16x8, pl[j]),
+                                                                       o[hh][4], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Stage st: start the direct loads of stage st + 1 into the other buffer
+    // (last read before the previous barrier), compute this wave's two tiles,
+    // then wait for this wave's loads and meet at the barrier.  Every stage
+    // holds NT tiles of the slab (n_tp is a multiple of NT); tiles past the
+    // block's last key are masked entirely (their keys exceed every query).
+    const int diag_from = a.prefix_len + q0 - (2 * KT - 1);  // tile pairs at or after this key need the mask
+    auto stage = [&](int st, const __bf16* cur, __bf16* nxt) {
+        if (st + 1 < n_stages) dma(st + 1, nxt);
+        const int ta = NT * st + 2 * part;
+        if (compute && ta < n_tiles) tile_pair(cur + 2 * part * kPrefillTileElems, ta * KT, ta * KT > diag_from);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct loads have landed
+        __syncthreads();
+    };
+
+    dma(0, buf0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    for (int st = 0; st < n_stages; st += 2) {
+        stage(st, buf0, buf1);
+        if (st + 1 < n_stages) stage(st + 1, buf1, buf0);
+    }
+
+    // Merge the two stage halves of each head: part 1 hands (m, l, O) to part 0
+    // through LDS (the stage buffers are free after the last barrier).  Pairs
+    // 0-1 use buf0, pairs 2-3 buf1: [pair % 2][head][18][64] floats.
+    static_assert(2 * 2 * 18 * 64 * 4 <= kStageElems * 2, "merge areas fit the stage buffers");
+    float* mgp = reinterpret_cast<float*>(pair < 2 ? buf0 : buf1) + (pair & 1) * 2 * 18 * 64;
+    float l[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) l[hh] = sum4_rows(g4 == 0 ? o[hh][4][0] : 0.f);
+    if (compute && part > 0) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            float* dst = mgp + hh * 18 * 64 + lane;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[(4 * db + i) * 64] = o[hh][db][i];
+            dst[16 * 64] = m[hh];
+            dst[17 * 64] = l[hh];
+        }
+    }
+    __syncthreads();
+    if (!compute || part > 0 || qi >= a.n_q) return;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        if (hh == 1 && 2 * pair + 1 >= G) break;
+        const float* src = mgp + hh * 18 * 64 + lane;
+        const float m1 = src[16 * 64], l1 = src[17 * 64];
+        const float mx = fmaxf(m[hh], m1);  // m[hh] is finite: part 0 holds tile 0, whose key 0 every query sees
+        const float a0 = fast_exp2((m[hh] - mx) * c);
+        const float a1 = (m1 == kNegInf) ? 0.f : fast_exp2((m1 - mx) * c);
+        const float inv = 1.f / (a0 * l[hh] + a1 * l1);
+        float* op = a.out + (((size_t)seq * a.n_q + qi) * NH + kv * G + hl[hh]) * kHeadDim + 4 * g4;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            float4 r;
+            r.x = (a0 * o[hh][db][0] + a1 * src[(4 * db + 0) * 64]) * inv;
+            r.y = (a0 * o[hh][db][1] + a1 * src[(4 * db + 1) * 64]) * inv;
+            r.z = (a0 * o[hh][db][2] + a1 * src[(4 * db + 2) * 64]) * inv;
+            r.w = (a0 * o[hh][db][3] + a1 * src[(4 * db + 3) * 64]) * inv;
+            *reinterpret_cast<float4*>(op + 16 * db) = r;
+        }
+    }
 }
 
 #define TMAC_PREFILL_KERNEL(G, KV)                                                                    \
@@ -865,6 +1078,14 @@ TMAC_PREFILL_KERNEL(2, 2)
 TMAC_PREFILL_KERNEL(4, 2)
 TMAC_PREFILL_KERNEL(4, 4)
 TMAC_PREFILL_KERNEL(8, 1)
+
+#define TMAC_PREFILL_PACK_KERNEL(KV)                                                                       \
+    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_kv##KV(PrefillArgs a) {            \
+        prefill_pack_body<KV>(a);                                                                         \
+    }
+TMAC_PREFILL_PACK_KERNEL(1)
+TMAC_PREFILL_PACK_KERNEL(2)
+TMAC_PREFILL_PACK_KERNEL(4)
 
 // RoPE in place, one lane per (head, pair): tmac_gguf.cpp:992-1003 for one
 // tensor, i.e. what rope_op (metal_backend.hpp:381) dispatches.

@@ -30,7 +30,10 @@ extern "C" const uint64_t tmac_attn_code_object_size;
 using tmac::CopyArgs;
 using tmac::DecodeArgs;
 using tmac::PrefillArgs;
+using tmac::kPrefillKeys;
 using tmac::kPrefillQueries;
+using tmac::kPrefillStageTiles;
+using tmac::kPrefillTileElems;
 using tmac::kPrefillWaves;
 using tmac::PosArgs;
 using tmac::RopeArgs;
@@ -72,6 +75,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head4[3];    // head kernel, 4 waves
     std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
+    std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr;
     float* ws = nullptr;
     size_t ws_floats = 0;
@@ -404,6 +408,12 @@ int tmac_init(tmac_context** out, int device) {
                 if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
                 ctx->prefill[{sh[0], sh[1]}] = f;
+                if (!ctx->prefill_pack.count(sh[1])) {
+                    std::snprintf(name, sizeof(name), "tmac_prefill_pack_kv%d", sh[1]);
+                    if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                        return bail(hip_fail(ctx, e, name));
+                    ctx->prefill_pack[sh[1]] = f;
+                }
             }
         }
     }
@@ -575,14 +585,28 @@ int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q
         return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: need n_seq, n_q, prefix_len >= 0");
     if (n_seq > 1 && seq_stride < (int64_t)prefix_len + n_q)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: seq_stride must cover prefix_len + n_q rows");
-    if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: n_seq exceeds 65535");
+    if ((int64_t)((n_q + kPrefillQueries - 1) / kPrefillQueries) * n_kv_head * n_seq > INT_MAX)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: too many (query block, kv head, sequence) units");
     if (n_seq == 0 || n_q == 0) return TMAC_OK;
     auto it = ctx->prefill.find({n_head / n_kv_head, n_kv_head});
     if (it == ctx->prefill.end()) return fail(ctx, TMAC_ERR_UNSUPPORTED, "prefill: unsupported group");
     if ((rc = set_device(ctx))) return rc;
-    PrefillArgs a{q, k_cache, v_cache, out, seq_stride, n_q, prefix_len, kQScale};
-    return launch(ctx, it->second, (unsigned)((n_q + kPrefillQueries - 1) / kPrefillQueries), (unsigned)n_kv_head,
-                  kPrefillWaves * 64, (hipStream_t)stream, &a, (unsigned)n_seq);
+    // bf16 tiles of rows 0 .. prefix_len + n_q - 1 per (sequence, kv head), in
+    // the split-KV workspace, then the attention over them.
+    const int n_qblk = (n_q + kPrefillQueries - 1) / kPrefillQueries;
+    const int n_rows = prefix_len + n_q;
+    const int n_tp = ((n_rows + kPrefillKeys - 1) / kPrefillKeys + kPrefillStageTiles - 1) / kPrefillStageTiles *
+                     kPrefillStageTiles;
+    const int64_t pack_blocks = (int64_t)n_tp * n_kv_head * n_seq;
+    if (pack_blocks > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: too many cache tiles");
+    const size_t pack_bytes = (size_t)pack_blocks * kPrefillTileElems * sizeof(uint16_t);
+    if ((rc = ensure_workspace(ctx, (hipStream_t)stream, pack_bytes / sizeof(float)))) return rc;
+    PrefillArgs a{q, k_cache, v_cache, out, seq_stride, n_q, prefix_len, n_qblk, kQScale,
+                  reinterpret_cast<uint16_t*>(ctx->ws), n_tp, n_rows};
+    if ((rc = launch(ctx, ctx->prefill_pack.at(n_kv_head), (unsigned)pack_blocks, 1, 256, (hipStream_t)stream, &a)))
+        return rc;
+    return launch(ctx, it->second, (unsigned)((int64_t)n_qblk * n_kv_head * n_seq), 1, kPrefillWaves * 64,
+                  (hipStream_t)stream, &a);
 }
 
 int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add) {
