@@ -143,7 +143,12 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
  * hold the chunk's rotated k and v).  q/out [n_seq][n_q][n_head][64]; sequence s
  * starts at row s * seq_stride.  QK^T and PV run on bf16 MFMA (q, k, v rounded
  * to bf16, fp32 accumulation, P split into bf16 hi + lo); with bf16-exact
- * inputs the result matches the fp32 CPU path within the fp32 tolerance. */
+ * inputs the result matches the fp32 CPU path within the fp32 tolerance.
+ * Two launches: the rows 0..prefix_len + n_q - 1 are first packed to bf16 tiles
+ * in the context's workspace (n_seq * n_kv_head * 16 KiB per 64 rows, rounded
+ * up to 256 rows), which grows on demand; a call that needs it to grow while
+ * the stream is capturing returns TMAC_ERR_CAPTURE, so run the largest shape
+ * once before capture. */
 int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
                            const float* v_cache, float* out, int n_seq, int n_q, int prefix_len,
                            int64_t seq_stride, int n_head, int n_kv_head, int head_dim);

@@ -84,3 +84,36 @@ def test_prefill_rejects_bad_arguments(ctx):
     assert ctx.prefill(d, d, d, d, 2, 16, 10, 20, 14, 2, HD, check=False) == tmac_attn.TMAC_ERR_INVALID_ARG
     assert ctx.prefill(d, d, d, d, 1, 16, 0, 16, 14, 2, 32, check=False) == tmac_attn.TMAC_ERR_UNSUPPORTED
     assert ctx.prefill(d, d, d, d, 1, 16, 0, 16, 14, 3, HD, check=False) == tmac_attn.TMAC_ERR_INVALID_ARG
+
+
+def test_prefill_graph_replay_matches_eager(ctx):
+    """Both prefill launches (tile pack + attention) captured into a graph: every
+    replay, with eager calls and new queries in between, equals the eager call
+    on the same inputs bit for bit, and the first also the oracle."""
+    n_seq, n_q, prefix, cap = 2, 40, 70, 120
+    q, k, v = (bf16_round(a) for a in make(700, n_seq, n_q, prefix, cap, 14, 2))
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    out_e = ctx.empty((n_seq, n_q, 14 * HD))
+    out_g = ctx.empty((n_seq, n_q, 14 * HD))
+    s = ctx.stream()
+    ctx.prefill(dq, dk, dv, out_e, n_seq, n_q, prefix, cap, 14, 2, HD, stream=s)  # sizes the workspace
+    ctx.synchronize(s)
+    ctx.step_begin(s)
+    ctx.prefill(dq, dk, dv, out_g, n_seq, n_q, prefix, cap, 14, 2, HD, stream=s)
+    g = ctx.step_end(s)
+    try:
+        for rep in range(3):
+            qn = bf16_round(oracle.normal(710 + rep, (n_seq, n_q, 14 * HD)))
+            dq.copy_from(qn)
+            ctx.prefill(dq, dk, dv, out_e, n_seq, n_q, prefix, cap, 14, 2, HD, stream=s)
+            ctx.synchronize(s)
+            ctx.graph_launch(g, s)
+            ctx.synchronize(s)
+            got = out_g.numpy()
+            np.testing.assert_array_equal(got, out_e.numpy(), err_msg=f"replay {rep}")
+            if rep == 0:
+                ref = oracle.prefill(qn, k, v, n_seq, n_q, prefix, cap, 14, 2, HD, n_threads=8)
+                assert_close(got, ref, "graph replay vs oracle")
+    finally:
+        ctx.graph_destroy(g)
+        ctx.destroy_stream(s)
