@@ -232,6 +232,73 @@ C5_FLOPS = 13_157_007_360  # 4 seqs x 14 heads x sum_{i<512} (1537 + i) rows x 4
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
+QKV_SHAPE = (896, 128, 128, 896)  # q rows, k rows, v rows, inputs (Qwen2-0.5B)
+
+
+def qkv_weight_bytes(v_is_q8: bool = True) -> int:
+    nq, nk, nv, cols = QKV_SHAPE
+    nb = cols // 32
+    return (nq + nk) * nb * 22 + nv * nb * (34 if v_is_q8 else 22)
+
+
+def bench_qkv(ctx, stream, steps, warmup, layers=24, sets=16):
+    """QKV projection (tmac_fused_qkv_bias) at the Qwen2-0.5B shape, Q5_0 q/k,
+    Q8_0 v.  (1) a graph of `layers` calls on one layer's weights: us/call.
+    (2) `sets` copies of all `layers` layers' weights (more bytes than the
+    Infinity Cache holds), one graph of `layers` launches per set, all sets in
+    turn: us/layer and weight-streaming GB/s."""
+    nq, nk, nv, cols = QKV_SHAPE
+    nb = cols // 32
+    rng = np.random.default_rng(6)
+    per_layer = qkv_weight_bytes()
+    n_inst = layers * sets
+
+    def blocks(rows, bb):
+        raw = rng.integers(0, 256, (rows * nb, bb), dtype=np.uint8)
+        raw[:, 0:2] = (rng.uniform(0.0005, 0.004, rows * nb).astype(np.float16)).view(np.uint8).reshape(-1, 2)
+        return raw.reshape(-1)
+
+    # one weight pool per matrix: instance i at offset i * (matrix bytes)
+    wq = ctx.upload(np.concatenate([blocks(nq, 22) for _ in range(n_inst)]))
+    wk = ctx.upload(np.concatenate([blocks(nk, 22) for _ in range(n_inst)]))
+    wv = ctx.upload(np.concatenate([blocks(nv, 34) for _ in range(n_inst)]))
+    x = ctx.upload(rng.standard_normal(cols).astype(np.float32))
+    b = [ctx.upload(rng.standard_normal(n).astype(np.float32)) for n in (nq, nk, nv)]
+    y = [ctx.empty(n) for n in (nq, nk, nv)]
+    bq, bk, bv = nq * nb * 22, nk * nb * 22, nv * nb * 34
+
+    def call(i):
+        ctx.fused_qkv(wq.ptr + i * bq, wk.ptr + i * bk, wv.ptr + i * bv, x, y[0], y[1], y[2], nq, nk, nv, cols,
+                      True, b_q=b[0], b_k=b[1], b_v=b[2], stream=stream)
+
+    # Launches are captured into graphs (as an engine's decode step would be),
+    # so host-side call overhead stays out of the timed region.
+    def capture(insts):
+        ctx.step_begin(stream)
+        for i in insts:
+            call(i)
+        return ctx.step_end(stream)
+
+    hot = capture([0] * layers)
+    graphs = [capture(range(st * layers, (st + 1) * layers)) for st in range(sets)]
+    per, mean_ms = time_launches(ctx, stream, lambda: ctx.graph_launch(hot, stream), steps, warmup)
+
+    def sweep():  # every set once: n_inst launches, each on weights not touched since the last sweep
+        for g in graphs:
+            ctx.graph_launch(g, stream)
+
+    per_s, mean_s = time_launches(ctx, stream, sweep, max(3, steps // 20), 1)
+    for g in [hot] + graphs:
+        ctx.graph_destroy(g)
+    for d in [wq, wk, wv, x] + b + y:
+        d.free()
+    return {"us_per_call": mean_ms * 1e3 / layers, "median_us": float(np.median(per)) * 1e3 / layers,
+            "weight_bytes_per_call": per_layer,
+            "stream_us_per_layer": mean_s * 1e3 / n_inst,
+            "stream_gbs": per_layer * n_inst / (mean_s * 1e-3) / 1e9,
+            "stream_weight_bytes": per_layer * n_inst}
+
+
 def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
     """Config 5: chunked causal prefill on bf16 MFMA."""
     cap = prefix + n_q
@@ -331,8 +398,8 @@ def main():
     ap.add_argument("--target-groups", type=int, default=None, help="override TMAC_OPT_TARGET_GROUPS (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
-    ap.add_argument("--sections", default="c1,c2,c4,c5",
-                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5")
+    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv",
+                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -379,6 +446,10 @@ def main():
     if "c4" in sections:
         extra["c4"] = bench_c4(ctx, stream, max(10, args.steps // 2), args.warmup)
         log(f"[bench] C4 {extra['c4']['gbs']:.1f} GB/s")
+    if "qkv" in sections:
+        extra["qkv"] = bench_qkv(ctx, stream, args.steps, args.warmup)
+        log(f"[bench] QKV {extra['qkv']['us_per_call']:.2f} us/call (hot), "
+            f"{extra['qkv']['stream_us_per_layer']:.2f} us/layer streaming = {extra['qkv']['stream_gbs']:.0f} GB/s")
     if "c5" in sections:
         extra["c5"] = bench_c5(ctx, stream, max(10, args.steps // 2), args.warmup)
         log(f"[bench] C5 {extra['c5']['mean_us']:.1f} us, {extra['c5']['tflops']:.1f} TFLOP/s, "

@@ -1,7 +1,7 @@
 /*
  * tmac_attn.h -- C ABI of the MI355X (gfx950) attention hot path of
  * liuwantao3/tmac_gguf.cpp: GQA decode attention over the fp32 KV cache,
- * RoPE, and the KV-cache row write.
+ * RoPE, and the KV-cache row write, plus the QKV projection that feeds them.
  *
  * The reference engine calls three Metal dispatch helpers from its per-layer
  * loop (tmac_gguf.cpp:1562-1568), bracketed by metal_batch_begin/end:
@@ -13,8 +13,9 @@
  *
  * This header exports the same three operations with the same argument
  * meaning, plus context lifecycle, step capture (hipGraph, the analogue of the
- * one command buffer per decode step), a fused per-layer entry point and the
- * batched / ragged-split-KV extensions.
+ * one command buffer per decode step), a fused per-layer entry point, the
+ * batched / ragged-split-KV / prefill extensions, and the producer of the
+ * path's inputs: fused_qkv_op (metal_backend.hpp:456) with its bias adds.
  *
  * Conventions (all entry points):
  *  - Buffers are DEVICE pointers owned by the caller (allocate them with
@@ -48,7 +49,7 @@ enum tmac_status {
     TMAC_ERR_INVALID_ARG = 1,     /* bad shape or value (negative past_len, n_head % n_kv_head, ...) */
     TMAC_ERR_NULL_POINTER = 2,
     TMAC_ERR_MISALIGNED = 3,      /* q/k/v/out/cache rows must be 16-byte aligned */
-    TMAC_ERR_UNSUPPORTED = 4,     /* head_dim != 64, unsupported GQA group, elem_op op != 2 */
+    TMAC_ERR_UNSUPPORTED = 4,     /* head_dim != 64, unsupported GQA group, elem_op op 1 */
     TMAC_ERR_CAPACITY = 5,        /* position beyond the cache / RoPE table / workspace */
     TMAC_ERR_NOT_INITIALIZED = 6,
     TMAC_ERR_CAPTURE = 7,         /* needs an allocation while the stream is being captured */
@@ -89,10 +90,31 @@ int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, con
 int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads, int head_dim,
                  int pos, float base);
 
-/* elem_op, metal_backend.hpp:354-379.  Only op 2 (cache write:
- * data[i] = aux[i], i < dim; tmac_gguf.cpp:1090-1091) is on this path; op 0
- * (add) and op 1 (silu*up) return TMAC_ERR_UNSUPPORTED. */
+/* elem_op, metal_backend.hpp:354-379 (kernel_elem.metal:14-21), i < dim:
+ *   op 2, cache write  data[i] = aux[i]   (tmac_gguf.cpp:1090-1091, 1564-1565)
+ *   op 0, add          data[i] += aux[i]  (the bias adds, tmac_gguf.cpp:1484-1489)
+ * op 1 (silu * up) belongs to the FFN and returns TMAC_ERR_UNSUPPORTED. */
 int tmac_elem_op(tmac_context* ctx, tmac_stream stream, int op, float* data, const float* aux, int dim);
+
+/* ---- QKV projection, the producer of q / k_new / v_new ----
+ * fused_qkv_op, metal_backend.hpp:456-489 (kernel_fused_qkv.metal:8-67); the
+ * reference's CPU form is tmac_gguf.cpp:1046-1062.  y_q = W_q x, y_k = W_k x,
+ * y_v = W_v x in one launch.  Each W is rows x cols in GGML blocks of 32 along
+ * a row: W_q and W_k Q5_0 (22 bytes: fp16 d, u32 qh, u8 qs[16]); W_v Q8_0
+ * (34 bytes: fp16 d, i8 q[32]) when v_is_q8, else Q5_0 (tmac_gguf.cpp:240-250,
+ * 311-327).  cols must be a multiple of 32; x is 16-byte aligned and must not
+ * overlap an output; weights are 2-byte aligned.  Each output is the exact
+ * dequantised dot product rounded as an fp32 sum (the order of the sum differs
+ * from the reference's sequential loop only by rounding). */
+int tmac_fused_qkv_op(tmac_context* ctx, tmac_stream stream, const void* w_q, const void* w_k, const void* w_v,
+                      const float* x, float* y_q, float* y_k, float* y_v, int q_rows, int k_rows, int v_rows,
+                      int cols, int v_is_q8);
+/* Extension: the same plus the three bias adds that follow it
+ * (tmac_gguf.cpp:1484-1489, elem_op 0) in the same launch; a null bias is
+ * absent, as the reference skips a missing bias tensor. */
+int tmac_fused_qkv_bias(tmac_context* ctx, tmac_stream stream, const void* w_q, const void* w_k, const void* w_v,
+                        const float* x, const float* b_q, const float* b_k, const float* b_v, float* y_q, float* y_k,
+                        float* y_v, int q_rows, int k_rows, int v_rows, int cols, int v_is_q8);
 
 /* ---- fused per-layer step (one launch replaces rope_op x2 + elem_op(2) x2 + attention_op,
  *      tmac_gguf.cpp:1562-1568) ----

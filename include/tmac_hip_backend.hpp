@@ -9,6 +9,8 @@
 //   metal_backend::metal_batch_begin(ctx)            metal_backend.hpp:114-122
 //   metal_backend::rope_op(ctx, data, n_heads, head_dim, pos, base)      :381-396
 //   metal_backend::elem_op(ctx, 2, cache_row, src, dim)                  :354-379
+//   metal_backend::fused_qkv_op(ctx, Wq, Wk, Wv, x, q, k, v, ...)       :456-489
+//   metal_backend::elem_op(ctx, 0, q|k|v, bias, dim)  (bias adds, tmac_gguf.cpp:1484-1489)
 //   metal_backend::attention_op(ctx, Q, K, V, out, n_head, n_kv_head, head_dim, past_len) :413-453
 //   metal_backend::metal_batch_end()                 metal_backend.hpp:176-190
 //   metal_backend::shutdown(ctx)                     metal_backend.hpp:520
@@ -107,6 +109,23 @@ inline void rope_op(Context& c, float* data, int n_heads, int head_dim, int pos,
 
 inline void elem_op(Context& c, int op, float* data, const float* aux, int dim) {
     detail::note(c, tmac_elem_op(c.ctx, c.stream, op, data, aux, dim), "elem_op");
+}
+
+inline void fused_qkv_op(Context& c, const uint8_t* W_q, const uint8_t* W_k, const uint8_t* W_v, const float* x,
+                         float* y_q, float* y_k, float* y_v, int q_rows, int k_rows, int v_rows, int cols,
+                         bool v_is_q8) {
+    detail::note(c, tmac_fused_qkv_op(c.ctx, c.stream, W_q, W_k, W_v, x, y_q, y_k, y_v, q_rows, k_rows, v_rows,
+                                      cols, v_is_q8 ? 1 : 0),
+                 "fused_qkv_op");
+}
+
+// fused_qkv_op followed by the three bias adds, in one launch (null bias = absent).
+inline void fused_qkv_bias_op(Context& c, const uint8_t* W_q, const uint8_t* W_k, const uint8_t* W_v,
+                              const float* x, const float* b_q, const float* b_k, const float* b_v, float* y_q,
+                              float* y_k, float* y_v, int q_rows, int k_rows, int v_rows, int cols, bool v_is_q8) {
+    detail::note(c, tmac_fused_qkv_bias(c.ctx, c.stream, W_q, W_k, W_v, x, b_q, b_k, b_v, y_q, y_k, y_v, q_rows,
+                                        k_rows, v_rows, cols, v_is_q8 ? 1 : 0),
+                 "fused_qkv_bias_op");
 }
 
 // One launch for the whole slice rope q, rope k, write k, write v, attention.

@@ -70,6 +70,15 @@ def _load(path: str) -> ctypes.CDLL:
     lib.oracle_prefill.restype = ctypes.c_int
     lib.oracle_max_threads.argtypes = []
     lib.oracle_max_threads.restype = ctypes.c_int
+    lib.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.oracle_f16_to_f32.restype = ctypes.c_float
+    lib.oracle_dequant.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64]
+    lib.oracle_dequant.restype = ctypes.c_float
+    lib.oracle_matmul_q.argtypes = [ctypes.c_int, ctypes.c_void_p, _F, _F, ctypes.c_int, ctypes.c_int]
+    lib.oracle_matmul_q.restype = ctypes.c_int
+    lib.oracle_qkv.argtypes = ([ctypes.c_void_p] * 3 + [ctypes.c_int, _F] + [ctypes.c_void_p] * 3 + [_F] * 3 +
+                               [ctypes.c_int] * 4)
+    lib.oracle_qkv.restype = ctypes.c_int
     _libs[path] = lib
     return lib
 
@@ -198,3 +207,48 @@ def prefill(q, k_cache, v_cache, n_seq: int, n_q: int, prefix_len: int, seq_capa
 
 def max_threads(timing: bool = False) -> int:
     return lib(timing).oracle_max_threads()
+
+
+# ---- quantized weights (tmac_gguf.cpp:219-231, 240-250, 311-327, 510-514, 1046-1081) ----
+Q5_0, Q8_0 = 6, 8
+BLOCK_BYTES = {Q5_0: 22, Q8_0: 34}
+
+
+def _u8(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    return a
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().oracle_f16_to_f32(int(h) & 0xFFFF))
+
+
+def dequant(qtype: int, data, idx: int) -> float:
+    data = _u8(data)
+    return float(lib().oracle_dequant(qtype, data.ctypes.data, idx))
+
+
+def matmul_q(qtype: int, w, x, rows: int, cols: int) -> np.ndarray:
+    """y = W x with the reference's per-row sequential fp32 sum; W is `rows`
+    rows of cols/32 blocks of `qtype`."""
+    w = _u8(w)
+    x = _f32(x)
+    if w.size < rows * (cols // 32) * BLOCK_BYTES.get(qtype, 0) or x.size < cols:
+        raise ValueError("matmul_q: buffers too small")
+    y = np.empty(rows, dtype=np.float32)
+    if lib().oracle_matmul_q(qtype, w.ctypes.data, _fp(x), _fp(y), rows, cols) != 0:
+        raise ValueError("oracle_matmul_q: bad arguments")
+    return y
+
+
+def qkv(wq, wk, wv, v_is_q8: bool, x, bq, bk, bv, q_rows: int, k_rows: int, v_rows: int, cols: int):
+    """The QKV projection of one layer plus its biases (None = absent)."""
+    wq, wk, wv, x = _u8(wq), _u8(wk), _u8(wv), _f32(x)
+    bias = [None if b is None else _f32(b) for b in (bq, bk, bv)]
+    out = [np.empty(n, dtype=np.float32) for n in (q_rows, k_rows, v_rows)]
+    rc = lib().oracle_qkv(wq.ctypes.data, wk.ctypes.data, wv.ctypes.data, int(v_is_q8), _fp(x),
+                          *[None if b is None else b.ctypes.data for b in bias], *[_fp(o) for o in out],
+                          q_rows, k_rows, v_rows, cols)
+    if rc != 0:
+        raise ValueError("oracle_qkv: bad arguments")
+    return tuple(out)

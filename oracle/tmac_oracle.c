@@ -286,3 +286,65 @@ int oracle_prefill(const float* q, const float* k_cache, const float* v_cache, f
     free(units);
     return rc;
 }
+
+/* ---- quantized weights ---- */
+
+/* tmac_gguf.cpp:219-231: sign * (1 + mant/1024) * 2^(exp-15), subnormals
+ * mant/1024 * 2^-14, exp 31 -> inf / NaN. */
+float oracle_f16_to_f32(uint16_t f16) {
+    uint32_t sign = (f16 >> 15) & 0x1;
+    uint32_t ex = (f16 >> 10) & 0x1F;
+    uint32_t mant = f16 & 0x3FF;
+    if (ex == 0) {
+        if (mant == 0) return 0.0f;
+        return (sign ? -1.0f : 1.0f) * (mant / 1024.0f) * powf(2.0f, -14.0f);
+    }
+    if (ex == 31) return mant ? NAN : (sign ? -INFINITY : INFINITY);
+    return (sign ? -1.0f : 1.0f) * (1.0f + mant / 1024.0f) * powf(2.0f, (int)ex - 15);
+}
+
+/* tmac_gguf.cpp:240-250 (Q8_0) and 311-327 (Q5_0): the weight at flat index idx. */
+float oracle_dequant(int type, const uint8_t* data, uint64_t idx) {
+    const uint64_t block = idx / 32, e = idx % 32;
+    if (type == ORACLE_Q8_0) {
+        const uint8_t* b = data + block * 34;
+        const float d = oracle_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+        return (float)(int8_t)b[2 + e] * d;
+    }
+    const uint8_t* b = data + block * 22;
+    const float d = oracle_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+    const uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+    const uint8_t byte = b[6 + (e < 16 ? e : e - 16)];
+    const uint8_t ql = e < 16 ? (byte & 0xF) : (byte >> 4);
+    const int q = (int)((((qh >> e) & 1) << 4) | ql) - 16;
+    return d * (float)q;
+}
+
+/* tmac_gguf.cpp:510-514: one fp32 accumulator per row, inputs in ascending
+ * order, the product rounded before the add (no contraction in this build).
+ * read_tensor's flat index is col + row * cols (tmac_gguf.cpp:405). */
+int oracle_matmul_q(int type, const uint8_t* w, const float* x, float* y, int rows, int cols) {
+    if (!w || !x || !y || rows < 0 || cols <= 0 || cols % 32 || (type != ORACLE_Q5_0 && type != ORACLE_Q8_0))
+        return -1;
+    for (int i = 0; i < rows; i++) {
+        float sum = 0;
+        for (int j = 0; j < cols; j++) sum += oracle_dequant(type, w, (uint64_t)j + (uint64_t)i * cols) * x[j];
+        y[i] = sum;
+    }
+    return 0;
+}
+
+/* tmac_gguf.cpp:1046-1081: the three projections of the normed hidden state,
+ * then `out[i] += b[i]` for each bias that exists. */
+int oracle_qkv(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int v_is_q8, const float* x,
+               const float* bq, const float* bk, const float* bv, float* q, float* k, float* v,
+               int q_rows, int k_rows, int v_rows, int cols) {
+    if (oracle_matmul_q(ORACLE_Q5_0, wq, x, q, q_rows, cols) ||
+        oracle_matmul_q(ORACLE_Q5_0, wk, x, k, k_rows, cols) ||
+        oracle_matmul_q(v_is_q8 ? ORACLE_Q8_0 : ORACLE_Q5_0, wv, x, v, v_rows, cols))
+        return -1;
+    if (bq) for (int i = 0; i < q_rows; i++) q[i] += bq[i];
+    if (bk) for (int i = 0; i < k_rows; i++) k[i] += bk[i];
+    if (bv) for (int i = 0; i < v_rows; i++) v[i] += bv[i];
+    return 0;
+}

@@ -12,6 +12,10 @@
  *   cache reset   tmac_gguf.cpp:1430-1434  (memset 0)
  *   attention     tmac_gguf.cpp:1093-1128  (two-pass log-sum-exp softmax)
  *   constants     tmac_gguf.cpp:163-172    (Qwen2-0.5B: 14 q heads, 2 kv heads, head_dim 64)
+ *   fp16 decode   tmac_gguf.cpp:219-231    (f16_to_f32)
+ *   Q8_0 / Q5_0   tmac_gguf.cpp:240-250, 311-327 (dequant_q8_0 / dequant_q5_0)
+ *   matmul        tmac_gguf.cpp:405-414, 510-514 (read_tensor + the CPU row loop)
+ *   QKV + bias    tmac_gguf.cpp:1046-1081  (three matmuls on the normed hidden state, then bias adds)
  *
  * Generalisations (the reference hard-codes them): n_head / n_kv_head /
  * head_dim / base are arguments, the score buffer is sized by n_pos instead of
@@ -91,6 +95,24 @@ int oracle_prefill(const float* q, const float* k_cache, const float* v_cache, f
 
 /* Number of OpenMP threads the library was built with (1 without OpenMP). */
 int oracle_max_threads(void);
+
+/* ---- quantized weights: the producer of q / k_new / v_new ----
+ * Blocks of 32 weights along a row (GGML layout, rows of `cols` inputs):
+ *   Q8_0 (type 8): fp16 d, int8 q[32]                          34 bytes; w = q * d
+ *   Q5_0 (type 6): fp16 d, uint32 qh, uint8 qs[16]             22 bytes;
+ *                  element e: low nibble of qs[e] (e < 16) or high nibble of
+ *                  qs[e - 16], fifth bit = bit e of qh, w = d * (q5 - 16)     */
+enum { ORACLE_Q5_0 = 6, ORACLE_Q8_0 = 8 };
+float oracle_f16_to_f32(uint16_t h);
+float oracle_dequant(int type, const uint8_t* data, uint64_t idx);
+/* y[i] = sum over j ascending of w[i][j] * x[j], one fp32 accumulator per row. */
+int oracle_matmul_q(int type, const uint8_t* w, const float* x, float* y, int rows, int cols);
+/* q = Wq x (+ bq), k = Wk x (+ bk), v = Wv x (+ bv); Wq, Wk are Q5_0, Wv is Q8_0
+ * when v_is_q8 else Q5_0; a null bias is skipped, as the reference skips an
+ * absent tensor. */
+int oracle_qkv(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int v_is_q8, const float* x,
+               const float* bq, const float* bk, const float* bv, float* q, float* k, float* v,
+               int q_rows, int k_rows, int v_rows, int cols);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,149 @@
+"""GPU parity of the QKV projection (tmac_fused_qkv_op / tmac_fused_qkv_bias)
+and of elem_op op 0 against the oracle (tmac_gguf.cpp:1046-1081, 510-514).
+
+Bars:
+- integer-valued weights and inputs (the reference's own Q8_0 test pattern,
+  test_q8_simdtc.mm:43-56, and a Q5_0 analogue) make every partial sum an exact
+  integer, so the GPU result must equal the oracle bit for bit whatever the
+  summation order;
+- real-valued weights at the magnitudes of a Q5_0 Qwen2-0.5B checkpoint
+  (|d| <= 0.004) use the fp32 tolerance |gpu - ref| <= 2e-5 + 1e-4 |ref|;
+- large-magnitude weights use the summation bound of two fp32 sums in different
+  orders: |gpu - ref| <= 2 * (cols + 1) * 2^-24 * sum_j |w_j x_j|.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import tmac_attn
+from conftest import assert_close
+from test_oracle_quant import dequant_f64, q5_block, random_blocks, reference_q8_pattern
+
+pytestmark = pytest.mark.gpu
+F16_ONE = 0x3C00
+
+
+def q5_integer_pattern(rows: int, cols: int, salt: int = 0):
+    nb = cols // 32
+    w = bytearray()
+    wi = np.empty((rows, cols), dtype=np.int64)
+    for r in range(rows):
+        for b in range(nb):
+            codes = [(r * 7 + b * 5 + 3 * l + salt) % 32 for l in range(32)]
+            wi[r, 32 * b:32 * b + 32] = np.array(codes) - 16
+            w += q5_block(F16_ONE, codes)
+    return np.frombuffer(bytes(w), dtype=np.uint8), wi
+
+
+def run_qkv(ctx, wq, wk, wv, x, nq, nk, nv, cols, v_is_q8, bias=(None, None, None), with_bias=None):
+    dw = [ctx.upload(w) if w is not None and w.size else None for w in (wq, wk, wv)]
+    dx = ctx.upload(x)
+    dy = [ctx.empty(max(n, 1)) for n in (nq, nk, nv)]
+    db = [None if b is None else ctx.upload(b) for b in bias]
+    ctx.fused_qkv(dw[0], dw[1], dw[2], dx, dy[0], dy[1], dy[2], nq, nk, nv, cols, v_is_q8,
+                  b_q=db[0], b_k=db[1], b_v=db[2], with_bias=with_bias)
+    out = [d.numpy()[:n] for d, n in zip(dy, (nq, nk, nv))]
+    for d in dw + [dx] + dy + db:
+        if d is not None:
+            d.free()
+    return out
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 64), (8, 896), (128, 64), (128, 896), (896, 896)])
+def test_q8_0_reference_pattern_bit_exact(ctx, rows, cols):
+    """The reference's Q8_0 GEMV test (scale 1, integer weights and inputs) on the V segment."""
+    w, x, wi = reference_q8_pattern(rows, cols)
+    _, _, got = run_qkv(ctx, None, None, w, x, 0, 0, rows, cols, True)
+    np.testing.assert_array_equal(got, oracle.matmul_q(oracle.Q8_0, w, x, rows, cols))
+    np.testing.assert_array_equal(got, (wi @ x.astype(np.int64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 64), (37, 896), (128, 2048), (5, 32)])
+def test_q5_0_integer_pattern_bit_exact(ctx, rows, cols):
+    wq, wiq = q5_integer_pattern(rows, cols)
+    wk, wik = q5_integer_pattern(3, cols, salt=1)
+    wv, wiv = q5_integer_pattern(2, cols, salt=2)
+    x = np.array([i % 7 - 3 for i in range(cols)], dtype=np.float32)
+    q, k, v = run_qkv(ctx, wq, wk, wv, x, rows, 3, 2, cols, False)
+    for got, wi, name in ((q, wiq, "q"), (k, wik, "k"), (v, wiv, "v")):
+        np.testing.assert_array_equal(got, (wi @ x.astype(np.int64)).astype(np.float32), err_msg=name)
+
+
+def qwen_like(rng, qtype, rows, cols):
+    w = random_blocks(rng, qtype, rows, cols)
+    nb = rows * (cols // 32)
+    blk = w.reshape(nb, oracle.BLOCK_BYTES[qtype])
+    d = (rng.uniform(0.0005, 0.004, nb) * rng.choice([-1, 1], nb)).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(-1)
+
+
+@pytest.mark.parametrize("v_is_q8", [True, False])
+def test_qwen2_shape_with_bias_matches_oracle(ctx, v_is_q8):
+    """One layer at the Qwen2-0.5B shape: 896 q rows, 128 k, 128 v, 896 inputs, biases."""
+    rng = np.random.default_rng(21 + v_is_q8)
+    cols, nq, nk, nv = 896, 896, 128, 128
+    wq = qwen_like(rng, oracle.Q5_0, nq, cols)
+    wk = qwen_like(rng, oracle.Q5_0, nk, cols)
+    wv = qwen_like(rng, oracle.Q8_0 if v_is_q8 else oracle.Q5_0, nv, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    bias = tuple(rng.standard_normal(n).astype(np.float32) * 0.1 for n in (nq, nk, nv))
+    got = run_qkv(ctx, wq, wk, wv, x, nq, nk, nv, cols, v_is_q8, bias)
+    ref = oracle.qkv(wq, wk, wv, v_is_q8, x, *bias, nq, nk, nv, cols)
+    for g, r, name in zip(got, ref, "qkv"):
+        assert_close(g, r, f"{name} (v_is_q8={v_is_q8})")
+    # without bias: the other entry point
+    got0 = run_qkv(ctx, wq, wk, wv, x, nq, nk, nv, cols, v_is_q8)
+    ref0 = oracle.qkv(wq, wk, wv, v_is_q8, x, None, None, None, nq, nk, nv, cols)
+    for g, r, name in zip(got0, ref0, "qkv"):
+        assert_close(g, r, f"{name} no bias (v_is_q8={v_is_q8})")
+
+
+@pytest.mark.parametrize("qtype", [oracle.Q5_0, oracle.Q8_0])
+def test_large_magnitude_within_summation_bound(ctx, qtype):
+    rng = np.random.default_rng(31 + qtype)
+    rows, cols = 77, 1536
+    w = random_blocks(rng, qtype, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    _, _, got = run_qkv(ctx, None, None, w, x, 0, 0, rows, cols, qtype == oracle.Q8_0)
+    ref = oracle.matmul_q(qtype, w, x, rows, cols)
+    scale = np.abs(dequant_f64(qtype, w, rows, cols)) @ np.abs(x.astype(np.float64))
+    bound = 2 * (cols + 1) * 2.0 ** -24 * scale
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= bound)
+
+
+def test_partial_biases_and_ragged_row_counts(ctx):
+    """Row totals that do not fill the last workgroup, a missing k bias."""
+    rng = np.random.default_rng(41)
+    cols, nq, nk, nv = 96, 13, 5, 3
+    wq, wk = qwen_like(rng, oracle.Q5_0, nq, cols), qwen_like(rng, oracle.Q5_0, nk, cols)
+    wv = qwen_like(rng, oracle.Q8_0, nv, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    bq, bv = rng.standard_normal(nq).astype(np.float32), rng.standard_normal(nv).astype(np.float32)
+    got = run_qkv(ctx, wq, wk, wv, x, nq, nk, nv, cols, True, (bq, None, bv))
+    ref = oracle.qkv(wq, wk, wv, True, x, bq, None, bv, nq, nk, nv, cols)
+    for g, r, name in zip(got, ref, "qkv"):
+        assert_close(g, r, name)
+
+
+def test_rejects_bad_arguments(ctx):
+    d = ctx.empty(1024)
+    qkv = lambda **kw: ctx.fused_qkv(*(kw.get(n, d) for n in ("wq", "wk", "wv", "x", "yq", "yk", "yv")),
+                                      kw.get("nq", 4), kw.get("nk", 4), kw.get("nv", 4), kw.get("cols", 64),
+                                      True, check=False)
+    assert qkv(cols=48) == tmac_attn.TMAC_ERR_INVALID_ARG
+    assert qkv(cols=0) == tmac_attn.TMAC_ERR_INVALID_ARG
+    assert qkv(nq=-1) == tmac_attn.TMAC_ERR_INVALID_ARG
+    assert qkv(wk=None) == tmac_attn.TMAC_ERR_NULL_POINTER
+    assert qkv(x=d.at(1)) == tmac_attn.TMAC_ERR_MISALIGNED
+    assert qkv(nq=0, nk=0, nv=0) == tmac_attn.TMAC_OK
+
+
+def test_elem_op_add_bit_exact(ctx):
+    rng = np.random.default_rng(51)
+    a = rng.standard_normal(1000).astype(np.float32)
+    b = rng.standard_normal(1000).astype(np.float32)
+    da, db = ctx.upload(a), ctx.upload(b)
+    ctx.elem_op(0, da, db, 1000)
+    np.testing.assert_array_equal(da.numpy(), a + b)
+    assert ctx.elem_op(1, da, db, 1000, check=False) == tmac_attn.TMAC_ERR_UNSUPPORTED

@@ -84,7 +84,22 @@ struct CopyArgs {
     float* dst;
     const float* src;
     int n;
+    int add;                 // 0: dst = src (elem_op 2), 1: dst += src (elem_op 0)
 };
+
+// QKV projection of one layer: y[s] = W[s] x (+ bias[s]) for s = q, k, v.
+// W[s] is rows[s] rows of cols / 32 blocks; q and k are Q5_0, v is Q8_0 when
+// v_is_q8, else Q5_0.  A null bias is absent.
+struct QkvArgs {
+    const uint8_t* w[3];
+    const float* x;          // [cols], 16-byte aligned
+    const float* bias[3];
+    float* y[3];
+    int rows[3];
+    int cols;
+    int v_is_q8;
+};
+constexpr int kQkvWaves = 4;         // output rows per workgroup (one wave each)
 
 struct PosArgs {
     int* pos;

@@ -1087,6 +1087,96 @@ TMAC_PREFILL_PACK_KERNEL(1)
 TMAC_PREFILL_PACK_KERNEL(2)
 TMAC_PREFILL_PACK_KERNEL(4)
 
+// ---------------------------------------------------------------------------
+// QKV projection: the producer of q / k_new / v_new (fused_qkv_op,
+// metal_backend.hpp:456-489; CPU form tmac_gguf.cpp:1046-1081, dequantisation
+// tmac_gguf.cpp:240-250 and 311-327).  y = W x (+ b) for the three weight
+// matrices of a layer in one launch, one wave per output row.  Lane u of a row
+// takes half of block u / 2: for Q5_0 the elements 8h + i and 16 + 8h + i
+// (i < 8; byte 8h + i of qs holds both nibbles), for Q8_0 the elements 16h + i
+// (i < 16).  Every block field sits at an even offset, so the weights are read
+// as 16-bit words.  The dequantised weight d * q is exact in fp32; the row sum
+// is one fused multiply-add per element, then a wave reduction, so it differs
+// from the reference's sequential sum only by rounding.
+__device__ __forceinline__ float wave_sum(float x) {
+    x = slot_sum(x);
+    x += dpp<0x140>(x);  // row_mirror: lane i <- lane 15 - i, the other 8-lane half
+    return sum4_rows(x);
+}
+
+__device__ __forceinline__ unsigned ld16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+__device__ __forceinline__ float half_bits_to_float(unsigned h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+}
+
+extern "C" __global__ __launch_bounds__(kQkvWaves * 64) void tmac_qkv(QkvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int r = blockIdx.x * kQkvWaves + wave;
+    int seg = 0;
+    if (r >= a.rows[0]) {
+        r -= a.rows[0];
+        seg = 1;
+        if (r >= a.rows[1]) {
+            r -= a.rows[1];
+            seg = 2;
+            if (r >= a.rows[2]) return;
+        }
+    }
+    const bool q8 = seg == 2 && a.v_is_q8;
+    const int nb = a.cols >> 5;
+    const int bytes = q8 ? 34 : 22;
+    const uint8_t* wrow = a.w[seg] + (size_t)r * nb * bytes;
+    float acc = 0.f;
+    for (int u = lane; u < 2 * nb; u += 64) {
+        const int b = u >> 1, h = u & 1;
+        const uint8_t* blk = wrow + (size_t)b * bytes;
+        const float d = half_bits_to_float(ld16(blk));
+        const float* xb = a.x + 32 * b;
+        if (q8) {
+            const float4 x0 = *reinterpret_cast<const float4*>(xb + 16 * h);
+            const float4 x1 = *reinterpret_cast<const float4*>(xb + 16 * h + 4);
+            const float4 x2 = *reinterpret_cast<const float4*>(xb + 16 * h + 8);
+            const float4 x3 = *reinterpret_cast<const float4*>(xb + 16 * h + 12);
+            const float xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                                  x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const unsigned pr = ld16(blk + 2 + 16 * h + 2 * i);
+                acc = __builtin_fmaf((float)(int8_t)(pr & 0xFF) * d, xv[2 * i], acc);
+                acc = __builtin_fmaf((float)(int8_t)(pr >> 8) * d, xv[2 * i + 1], acc);
+            }
+        } else {
+            const unsigned qh = ld16(blk + 2) | (ld16(blk + 4) << 16);
+            const float4 l0 = *reinterpret_cast<const float4*>(xb + 8 * h);
+            const float4 l1 = *reinterpret_cast<const float4*>(xb + 8 * h + 4);
+            const float4 h0 = *reinterpret_cast<const float4*>(xb + 16 + 8 * h);
+            const float4 h1 = *reinterpret_cast<const float4*>(xb + 16 + 8 * h + 4);
+            const float xl[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            const float xh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned pr = ld16(blk + 6 + 8 * h + 2 * i);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int j = 8 * h + 2 * i + t;  // element j and j + 16
+                    const unsigned byte = (pr >> (8 * t)) & 0xFF;
+                    const int qlo = (int)((byte & 0xF) | (((qh >> j) & 1) << 4)) - 16;
+                    const int qhi = (int)((byte >> 4) | (((qh >> (j + 16)) & 1) << 4)) - 16;
+                    acc = __builtin_fmaf(d * (float)qlo, xl[2 * i + t], acc);
+                    acc = __builtin_fmaf(d * (float)qhi, xh[2 * i + t], acc);
+                }
+            }
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+        const float* bias = a.bias[seg];
+        a.y[seg][r] = bias ? acc + bias[r] : acc;
+    }
+}
+
 // RoPE in place, one lane per (head, pair): tmac_gguf.cpp:992-1003 for one
 // tensor, i.e. what rope_op (metal_backend.hpp:381) dispatches.
 extern "C" __global__ __launch_bounds__(256) void tmac_rope(RopeArgs a) {
@@ -1105,10 +1195,11 @@ extern "C" __global__ __launch_bounds__(256) void tmac_rope(RopeArgs a) {
     *p = x;
 }
 
-// dst[i] = src[i]: the cache-row write of elem_op(2, ...) (kernel_elem op 2).
+// dst[i] = src[i]: the cache-row write of elem_op(2, ...); dst[i] += src[i]:
+// the bias / residual add of elem_op(0, ...) (kernel_elem ops 2 and 0).
 extern "C" __global__ __launch_bounds__(256) void tmac_copy(CopyArgs a) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < a.n) a.dst[i] = a.src[i];
+    if (i < a.n) a.dst[i] = a.add ? a.dst[i] + a.src[i] : a.src[i];
 }
 
 // Device-side position for graph replays: *pos = value, or *pos += value.

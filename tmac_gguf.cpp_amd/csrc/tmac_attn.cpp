@@ -36,6 +36,8 @@ using tmac::kPrefillStageTiles;
 using tmac::kPrefillTileElems;
 using tmac::kPrefillWaves;
 using tmac::PosArgs;
+using tmac::QkvArgs;
+using tmac::kQkvWaves;
 using tmac::RopeArgs;
 using tmac::kHeadDim;
 using tmac::kPartialStride;
@@ -76,7 +78,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
-    hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr;
+    hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr;
     float* ws = nullptr;
     size_t ws_floats = 0;
     int* err = nullptr;
@@ -419,7 +421,8 @@ int tmac_init(tmac_context** out, int device) {
     }
     if ((e = hipModuleGetFunction(&ctx->k_rope, ctx->module, "tmac_rope")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->k_copy, ctx->module, "tmac_copy")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_pos, ctx->module, "tmac_pos_update")) != hipSuccess)
+        (e = hipModuleGetFunction(&ctx->k_pos, ctx->module, "tmac_pos_update")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->k_qkv, ctx->module, "tmac_qkv")) != hipSuccess)
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
@@ -650,14 +653,52 @@ int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads
 int tmac_elem_op(tmac_context* ctx, tmac_stream stream, int op, float* data, const float* aux, int dim) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
-    if (op != 2)
-        return fail(ctx, TMAC_ERR_UNSUPPORTED, "elem_op: only op 2 (cache write) is on the attention path");
+    if (op != 0 && op != 2)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED,
+                    "elem_op: op 0 (add: bias, residual) and op 2 (cache write) are supported; op 1 is the FFN");
     if (!data || !aux) return fail(ctx, TMAC_ERR_NULL_POINTER, "elem_op: null buffer");
     if (dim < 0) return fail(ctx, TMAC_ERR_INVALID_ARG, "elem_op: dim < 0");
     if (dim == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
-    CopyArgs a{data, aux, dim};
+    CopyArgs a{data, aux, dim, op == 0 ? 1 : 0};
     return launch(ctx, ctx->k_copy, (unsigned)((dim + 255) / 256), 1, 256, (hipStream_t)stream, &a);
+}
+
+static int qkv_common(tmac_context* ctx, hipStream_t stream, const void* w_q, const void* w_k, const void* w_v,
+                      const float* x, const float* b_q, const float* b_k, const float* b_v, float* y_q,
+                      float* y_k, float* y_v, int q_rows, int k_rows, int v_rows, int cols, int v_is_q8) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (q_rows < 0 || k_rows < 0 || v_rows < 0 || cols <= 0 || cols % 32)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "fused_qkv: rows >= 0 and cols a positive multiple of 32");
+    const int64_t total = (int64_t)q_rows + k_rows + v_rows;
+    if (total + kQkvWaves > INT_MAX || (int64_t)cols * 2 > INT_MAX)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "fused_qkv: too many rows");
+    if (!x || (q_rows && (!w_q || !y_q)) || (k_rows && (!w_k || !y_k)) || (v_rows && (!w_v || !y_v)))
+        return fail(ctx, TMAC_ERR_NULL_POINTER, "fused_qkv: null buffer");
+    if (!aligned16(x) || ((uintptr_t)w_q | (uintptr_t)w_k | (uintptr_t)w_v) % 2 ||
+        ((uintptr_t)y_q | (uintptr_t)y_k | (uintptr_t)y_v | (uintptr_t)b_q | (uintptr_t)b_k | (uintptr_t)b_v) % 4)
+        return fail(ctx, TMAC_ERR_MISALIGNED,
+                    "fused_qkv: x must be 16-byte aligned, weights 2-byte aligned, outputs and biases 4-byte");
+    if (total == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    QkvArgs a{{(const uint8_t*)w_q, (const uint8_t*)w_k, (const uint8_t*)w_v}, x, {b_q, b_k, b_v},
+              {y_q, y_k, y_v}, {q_rows, k_rows, v_rows}, cols, v_is_q8 ? 1 : 0};
+    return launch(ctx, ctx->k_qkv, (unsigned)((total + kQkvWaves - 1) / kQkvWaves), 1, kQkvWaves * 64, stream, &a);
+}
+
+int tmac_fused_qkv_op(tmac_context* ctx, tmac_stream stream, const void* w_q, const void* w_k, const void* w_v,
+                      const float* x, float* y_q, float* y_k, float* y_v, int q_rows, int k_rows, int v_rows,
+                      int cols, int v_is_q8) {
+    return qkv_common(ctx, (hipStream_t)stream, w_q, w_k, w_v, x, nullptr, nullptr, nullptr, y_q, y_k, y_v, q_rows,
+                      k_rows, v_rows, cols, v_is_q8);
+}
+
+int tmac_fused_qkv_bias(tmac_context* ctx, tmac_stream stream, const void* w_q, const void* w_k, const void* w_v,
+                        const float* x, const float* b_q, const float* b_k, const float* b_v, float* y_q, float* y_k,
+                        float* y_v, int q_rows, int k_rows, int v_rows, int cols, int v_is_q8) {
+    return qkv_common(ctx, (hipStream_t)stream, w_q, w_k, w_v, x, b_q, b_k, b_v, y_q, y_k, y_v, q_rows, k_rows,
+                      v_rows, cols, v_is_q8);
 }
 
 int tmac_set_option(tmac_context* ctx, int option, int64_t value) {

@@ -59,6 +59,8 @@ SIGNATURES = {
     "tmac_attention_op": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "tmac_rope_op": (_i, [_vp, _vp, _vp, _i, _i, _i, _f]),
     "tmac_elem_op": (_i, [_vp, _vp, _i, _vp, _vp, _i]),
+    "tmac_fused_qkv_op": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "tmac_fused_qkv_bias": (_i, [_vp] * 12 + [_i] * 5),
     "tmac_layer_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f]),
     "tmac_layer_attention_devpos": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _f]),
     "tmac_pos_update": (_i, [_vp, _vp, _vp, _i, _i]),
@@ -279,6 +281,23 @@ class Context:
         rc = self.lib.tmac_elem_op(self.handle, stream, op, _p(data), _p(aux), dim)
         if check:
             self._check(rc, "elem_op")
+        return rc
+
+    def fused_qkv(self, w_q, w_k, w_v, x, y_q, y_k, y_v, q_rows, k_rows, v_rows, cols, v_is_q8,
+                  b_q=None, b_k=None, b_v=None, stream=None, check=True, with_bias=None) -> int:
+        """tmac_fused_qkv_bias when any bias is given (or with_bias is True), else
+        tmac_fused_qkv_op."""
+        if with_bias is None:
+            with_bias = any(b is not None for b in (b_q, b_k, b_v))
+        if with_bias:
+            rc = self.lib.tmac_fused_qkv_bias(self.handle, stream, _p(w_q), _p(w_k), _p(w_v), _p(x), _p(b_q),
+                                              _p(b_k), _p(b_v), _p(y_q), _p(y_k), _p(y_v), q_rows, k_rows,
+                                              v_rows, cols, int(v_is_q8))
+        else:
+            rc = self.lib.tmac_fused_qkv_op(self.handle, stream, _p(w_q), _p(w_k), _p(w_v), _p(x), _p(y_q),
+                                            _p(y_k), _p(y_v), q_rows, k_rows, v_rows, cols, int(v_is_q8))
+        if check:
+            self._check(rc, "fused_qkv")
         return rc
 
     def layer_attention(self, q, k_new, v_new, k_cache, v_cache, out, n_head, n_kv_head, head_dim,
