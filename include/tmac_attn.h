@@ -116,6 +116,22 @@ int tmac_fused_qkv_bias(tmac_context* ctx, tmac_stream stream, const void* w_q, 
                         const float* x, const float* b_q, const float* b_k, const float* b_v, float* y_q, float* y_k,
                         float* y_v, int q_rows, int k_rows, int v_rows, int cols, int v_is_q8);
 
+/* ---- attention output projection, the consumer of the path's output ----
+ * matmul_q8_0 / matmul_q5_0, metal_backend.hpp:320-338 (mul_mat_q5_0.metal:6-37);
+ * the engine calls them through matmul() (tmac_gguf.cpp:476-490) for
+ * attn_output.weight (tmac_gguf.cpp:1497-1498).  y = W x, W rows x cols in
+ * Q8_0 / Q5_0 blocks as above; x 16-byte aligned, x and y disjoint. */
+enum tmac_weight_type { TMAC_Q5_0 = 6, TMAC_Q8_0 = 8 };  /* the reference's tensor type codes (tmac_gguf.cpp:179-181) */
+int tmac_matmul_q8_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y);
+int tmac_matmul_q5_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y);
+/* Extension: y += W x in one launch, i.e. the projection followed by the
+ * residual add elem_op(0, hidden, attn_out) (tmac_gguf.cpp:1497-1499):
+ * each y[i] is (W x)[i] rounded to fp32, then added to y[i]. */
+int tmac_matmul_add(tmac_context* ctx, tmac_stream stream, int qtype, int rows, int cols, const void* w,
+                    const float* x, float* y);
+
 /* ---- fused per-layer step (one launch replaces rope_op x2 + elem_op(2) x2 + attention_op,
  *      tmac_gguf.cpp:1562-1568) ----
  * Rotates q and k_new at `pos`, writes k (rotated) and v_new to row `pos` of

@@ -11,6 +11,8 @@
 //   metal_backend::elem_op(ctx, 2, cache_row, src, dim)                  :354-379
 //   metal_backend::fused_qkv_op(ctx, Wq, Wk, Wv, x, q, k, v, ...)       :456-489
 //   metal_backend::elem_op(ctx, 0, q|k|v, bias, dim)  (bias adds, tmac_gguf.cpp:1484-1489)
+//   metal_backend::matmul_q5_0 / matmul_q8_0(ctx, rows, cols, W, x, y)   :320-338
+//   metal_backend::elem_op(ctx, 0, hidden, attn_out, dim)  (residual, tmac_gguf.cpp:1499)
 //   metal_backend::attention_op(ctx, Q, K, V, out, n_head, n_kv_head, head_dim, past_len) :413-453
 //   metal_backend::metal_batch_end()                 metal_backend.hpp:176-190
 //   metal_backend::shutdown(ctx)                     metal_backend.hpp:520
@@ -126,6 +128,19 @@ inline void fused_qkv_bias_op(Context& c, const uint8_t* W_q, const uint8_t* W_k
     detail::note(c, tmac_fused_qkv_bias(c.ctx, c.stream, W_q, W_k, W_v, x, b_q, b_k, b_v, y_q, y_k, y_v, q_rows,
                                         k_rows, v_rows, cols, v_is_q8 ? 1 : 0),
                  "fused_qkv_bias_op");
+}
+
+inline void matmul_q8_0(Context& c, int rows, int cols, const uint8_t* w, const float* x, float* y) {
+    detail::note(c, tmac_matmul_q8_0(c.ctx, c.stream, rows, cols, w, x, y), "matmul_q8_0");
+}
+
+inline void matmul_q5_0(Context& c, int rows, int cols, const uint8_t* w, const float* x, float* y) {
+    detail::note(c, tmac_matmul_q5_0(c.ctx, c.stream, rows, cols, w, x, y), "matmul_q5_0");
+}
+
+// y += W x: the output projection and the residual add in one launch.
+inline void matmul_add_op(Context& c, int qtype, int rows, int cols, const uint8_t* w, const float* x, float* y) {
+    detail::note(c, tmac_matmul_add(c.ctx, c.stream, qtype, rows, cols, w, x, y), "matmul_add_op");
 }
 
 // One launch for the whole slice rope q, rope k, write k, write v, attention.

@@ -1,5 +1,6 @@
-"""GPU parity of the QKV projection (tmac_fused_qkv_op / tmac_fused_qkv_bias)
-and of elem_op op 0 against the oracle (tmac_gguf.cpp:1046-1081, 510-514).
+"""GPU parity of the QKV projection (tmac_fused_qkv_op / tmac_fused_qkv_bias),
+the output projection (tmac_matmul_q5_0 / _q8_0 / tmac_matmul_add) and
+elem_op op 0 against the oracle (tmac_gguf.cpp:1046-1081, 510-514, 1497-1499).
 
 Bars:
 - integer-valued weights and inputs (the reference's own Q8_0 test pattern,
@@ -147,3 +148,32 @@ def test_elem_op_add_bit_exact(ctx):
     ctx.elem_op(0, da, db, 1000)
     np.testing.assert_array_equal(da.numpy(), a + b)
     assert ctx.elem_op(1, da, db, 1000, check=False) == tmac_attn.TMAC_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("qtype", [oracle.Q5_0, oracle.Q8_0])
+def test_output_projection_and_residual(ctx, qtype):
+    """attn_output.weight (896 x 896) applied to the attention output, then the
+    residual add hidden += attn_out (tmac_gguf.cpp:1497-1499): the separate
+    matmul + elem_op(0) and the fused tmac_matmul_add give the same bits."""
+    rng = np.random.default_rng(61 + qtype)
+    n = 896
+    w = qwen_like(rng, qtype, n, n)
+    ctxv = rng.standard_normal(n).astype(np.float32)
+    hidden = rng.standard_normal(n).astype(np.float32)
+    ref = oracle.matmul_q(qtype, w, ctxv, n, n)
+    dw, dx, dy = ctx.upload(w), ctx.upload(ctxv), ctx.empty(n)
+    ctx.matmul(qtype, n, n, dw, dx, dy)
+    y = dy.numpy()
+    assert_close(y, ref, "matmul")
+    dh = ctx.upload(hidden)
+    ctx.elem_op(0, dh, dy, n)  # separate residual add
+    sep = dh.numpy()
+    np.testing.assert_array_equal(sep, hidden + y)
+    dh2 = ctx.upload(hidden)
+    ctx.matmul(qtype, n, n, dw, dx, dh2, accumulate=True)  # fused
+    np.testing.assert_array_equal(dh2.numpy(), sep)
+    assert_close(dh2.numpy(), hidden + ref, "fused residual vs oracle")
+    assert ctx.matmul(qtype, n, n, dw, dx, dx, check=False) == tmac_attn.TMAC_ERR_INVALID_ARG
+    assert ctx.matmul(7, n, n, dw, dx, dy, accumulate=True, check=False) == tmac_attn.TMAC_ERR_UNSUPPORTED
+    for d in (dw, dx, dy, dh, dh2):
+        d.free()

@@ -701,6 +701,35 @@ int tmac_fused_qkv_bias(tmac_context* ctx, tmac_stream stream, const void* w_q, 
                       v_rows, cols, v_is_q8);
 }
 
+// A single weight matrix runs as the third segment of the projection kernel
+// (rows of Q8_0 or Q5_0 blocks); the residual form passes y as its own bias.
+static int matmul_common(tmac_context* ctx, hipStream_t stream, int qtype, int rows, int cols, const void* w,
+                         const float* x, float* y, bool accumulate) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (qtype != TMAC_Q5_0 && qtype != TMAC_Q8_0)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "matmul: weight type must be TMAC_Q5_0 or TMAC_Q8_0");
+    if (x && y && (const void*)x == (const void*)y)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "matmul: x and y must not overlap");
+    return qkv_common(ctx, stream, nullptr, nullptr, w, x, nullptr, nullptr, accumulate ? y : nullptr, nullptr,
+                      nullptr, y, 0, 0, rows, cols, qtype == TMAC_Q8_0);
+}
+
+int tmac_matmul_q8_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y) {
+    return matmul_common(ctx, (hipStream_t)stream, TMAC_Q8_0, rows, cols, w, x, y, false);
+}
+
+int tmac_matmul_q5_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y) {
+    return matmul_common(ctx, (hipStream_t)stream, TMAC_Q5_0, rows, cols, w, x, y, false);
+}
+
+int tmac_matmul_add(tmac_context* ctx, tmac_stream stream, int qtype, int rows, int cols, const void* w,
+                    const float* x, float* y) {
+    return matmul_common(ctx, (hipStream_t)stream, qtype, rows, cols, w, x, y, true);
+}
+
 int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
     int rc = check_ctx(ctx);
     if (rc) return rc;

@@ -32,6 +32,8 @@ TMAC_ERR_CAPTURE = 7
 TMAC_ERR_DEVICE_FAULT = 8
 TMAC_ERR_HIP_BASE = 1000
 
+TMAC_Q5_0 = 6
+TMAC_Q8_0 = 8
 TMAC_OPT_SPLIT_LEN = 1
 TMAC_OPT_TARGET_GROUPS = 2
 TMAC_OPT_KERNEL = 3
@@ -61,6 +63,9 @@ SIGNATURES = {
     "tmac_elem_op": (_i, [_vp, _vp, _i, _vp, _vp, _i]),
     "tmac_fused_qkv_op": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "tmac_fused_qkv_bias": (_i, [_vp] * 12 + [_i] * 5),
+    "tmac_matmul_q8_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "tmac_matmul_q5_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "tmac_matmul_add": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "tmac_layer_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f]),
     "tmac_layer_attention_devpos": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _f]),
     "tmac_pos_update": (_i, [_vp, _vp, _vp, _i, _i]),
@@ -298,6 +303,18 @@ class Context:
                                             _p(y_k), _p(y_v), q_rows, k_rows, v_rows, cols, int(v_is_q8))
         if check:
             self._check(rc, "fused_qkv")
+        return rc
+
+    def matmul(self, qtype, rows, cols, w, x, y, accumulate=False, stream=None, check=True) -> int:
+        """tmac_matmul_q5_0 / _q8_0 (y = W x), or tmac_matmul_add (y += W x)."""
+        if accumulate:
+            rc = self.lib.tmac_matmul_add(self.handle, stream, qtype, rows, cols, _p(w), _p(x), _p(y))
+        elif qtype == TMAC_Q8_0:
+            rc = self.lib.tmac_matmul_q8_0(self.handle, stream, rows, cols, _p(w), _p(x), _p(y))
+        else:
+            rc = self.lib.tmac_matmul_q5_0(self.handle, stream, rows, cols, _p(w), _p(x), _p(y))
+        if check:
+            self._check(rc, "matmul")
         return rc
 
     def layer_attention(self, q, k_new, v_new, k_cache, v_cache, out, n_head, n_kv_head, head_dim,
