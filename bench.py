@@ -108,6 +108,34 @@ def bench_c3(ctx, stream, steps, warmup, n_seq=256, n_pos=4096):
     return res, (q, k, v, out, n_seq, n_pos)
 
 
+def bench_kv16(ctx, stream, steps, warmup, dtype_name, n_seq=256, n_pos=4096):
+    """Config 3's workload on a 16-bit cache (tmac_attention_decode_batched_kv):
+    the same rows, half the bytes.  K/V are drawn as in config 3 and converted
+    on the device (tmac_kv_convert)."""
+    import tmac_attn
+    dt = {"bf16": tmac_attn.TMAC_KV_BF16, "f16": tmac_attn.TMAC_KV_F16}[dtype_name]
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((n_seq, NH * HD), dtype=np.float32)
+    dq, dout = ctx.upload(q), ctx.empty((n_seq, NH * HD))
+    dk16, dv16 = ctx.empty(n_seq * n_pos * KVD, np.uint16), ctx.empty(n_seq * n_pos * KVD, np.uint16)
+    for d16 in (dk16, dv16):
+        tmp = ctx.upload(rng.standard_normal((n_seq * n_pos, KVD), dtype=np.float32))
+        ctx.kv_convert(dt, tmp, d16, n_seq * n_pos * KVD)
+        ctx.synchronize()
+        tmp.free()
+
+    def launch():
+        ctx.decode_batched(dq, dk16, dv16, dout, n_seq, NH, NKV, HD, n_pos, n_pos, stream=stream, kv_dtype=dt)
+
+    per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
+    nbytes = n_seq * (n_pos * KVD * 2 * 2 + 2 * NH * HD * 4)  # K + V 16-bit, q + out fp32
+    for d in (dq, dout, dk16, dv16):
+        d.free()
+    return {"bytes": nbytes, "mean_us": mean_ms * 1e3, "median_us": float(np.median(per)) * 1e3,
+            "gbs": nbytes / (mean_ms * 1e-3) / 1e9, "pct_of_peak": nbytes / (mean_ms * 1e-3) / 1e9 / 80.0,
+            "rows_per_s": n_seq * n_pos / (mean_ms * 1e-3)}
+
+
 def bench_c1(ctx, stream, steps=200, warmup=20):
     rng = np.random.default_rng(1)
     q = rng.standard_normal(NH * HD, dtype=np.float32)
@@ -398,8 +426,8 @@ def main():
     ap.add_argument("--target-groups", type=int, default=None, help="override TMAC_OPT_TARGET_GROUPS (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
-    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv",
-                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv")
+    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv,kv16",
+                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv,kv16")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -446,6 +474,12 @@ def main():
     if "c4" in sections:
         extra["c4"] = bench_c4(ctx, stream, max(10, args.steps // 2), args.warmup)
         log(f"[bench] C4 {extra['c4']['gbs']:.1f} GB/s")
+    for tn in ("bf16", "f16"):
+        if "kv16" in sections or f"kv_{tn}" in sections:
+            extra[f"c3_{tn}"] = bench_kv16(ctx, stream, args.steps, args.warmup, tn)
+            r = extra[f"c3_{tn}"]
+            log(f"[bench] C3 {tn} cache: {r['mean_us']:.1f} us/launch, {r['gbs']:.1f} GB/s "
+                f"({r['pct_of_peak']:.1f}% of peak), {r['rows_per_s'] / 1e9:.2f} G rows/s")
     if "qkv" in sections:
         extra["qkv"] = bench_qkv(ctx, stream, args.steps, args.warmup)
         log(f"[bench] QKV {extra['qkv']['us_per_call']:.2f} us/call (hot), "

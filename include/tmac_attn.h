@@ -174,6 +174,33 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
                                  const int32_t* lengths, float* out, int n_seq, int n_head,
                                  int n_kv_head, int head_dim, int max_len, int64_t total_rows);
 
+/* ---- 16-bit KV caches (extension; the reduced-precision cache motivated at
+ *      LLAMACPP_METAL_STUDY.md:50-54) ----
+ * The same cache layout with bf16 or fp16 elements instead of fp32: half the
+ * bytes on the HBM-bound path.  Rows are read and widened exactly to fp32, so
+ * each call equals the fp32 path run on the widened cache (the tolerance
+ * contract: |out - oracle(widen(cache))| <= 2e-5 + 1e-4 |ref|).  The layer
+ * step rounds the rotated k and v_new to the cache type (nearest even) before
+ * it stores them and attends the stored values.  These calls use the default
+ * 8-wave group and head kernels whatever TMAC_OPT_GROUP_WAVES / _HEAD_WAVES say. */
+enum tmac_kv_dtype { TMAC_KV_F32 = 0, TMAC_KV_BF16 = 1, TMAC_KV_F16 = 2 };
+int tmac_attention_decode_batched_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                     const void* k, const void* v, float* out, int n_seq, int n_head,
+                                     int n_kv_head, int head_dim, int n_pos, int64_t seq_stride);
+int tmac_attention_decode_ragged_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                    const void* k_pool, const void* v_pool, const int64_t* offsets,
+                                    const int32_t* lengths, float* out, int n_seq, int n_head, int n_kv_head,
+                                    int head_dim, int max_len, int64_t total_rows);
+int tmac_layer_attention_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                            const float* k_new, const float* v_new, void* k_cache, void* v_cache, float* out,
+                            int n_head, int n_kv_head, int head_dim, int pos, int capacity, float base);
+int tmac_layer_attention_devpos_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                   const float* k_new, const float* v_new, void* k_cache, void* v_cache,
+                                   float* out, int n_head, int n_kv_head, int head_dim, const int* pos_dev,
+                                   int capacity, float base);
+/* dst[i] = src[i] rounded to nearest even in kv_dtype (BF16 or F16), i < n: fills a 16-bit cache. */
+int tmac_kv_convert(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* src, void* dst, int64_t n);
+
 /* ---- chunked causal prefill (extension; the reference feeds prompts one token at a time,
  *      tmac_gguf.cpp:1621-1658, so its oracle is attention_op per query row) ----
  * Query i of sequence s sits at position prefix_len + i and attends rows

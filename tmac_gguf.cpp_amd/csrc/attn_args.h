@@ -87,6 +87,14 @@ struct CopyArgs {
     int add;                 // 0: dst = src (elem_op 2), 1: dst += src (elem_op 0)
 };
 
+// fp32 -> 16-bit cache values (round to nearest even): dst[i] = T(src[i]).
+struct CvtArgs {
+    const float* src;
+    void* dst;
+    int64_t n;
+    int dtype;               // 1: bf16, 2: fp16
+};
+
 // QKV projection of one layer: y[s] = W[s] x (+ bias[s]) for s = q, k, v.
 // W[s] is rows[s] rows of cols / 32 blocks; q and k are Q5_0, v is Q8_0 when
 // v_is_q8, else Q5_0.  A null bias is absent.

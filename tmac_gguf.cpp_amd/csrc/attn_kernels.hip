@@ -86,6 +86,38 @@ __device__ __forceinline__ void store8(float* __restrict__ p, const float (&x)[8
     *reinterpret_cast<float4*>(p + 32) = make_float4(x[4], x[5], x[6], x[7]);
 }
 
+// 16-bit caches (bf16 / fp16, the same [row][kv][64] layout): a lane's 8 dims
+// are two 8-byte loads, widened exactly to fp32; stores round to nearest even.
+template <typename T>
+__device__ __forceinline__ void load8(float (&x)[8], const T* __restrict__ p) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 a = *reinterpret_cast<const t4*>(p);
+    const t4 b = *reinterpret_cast<const t4*>(p + 32);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        x[t] = (float)a[t];
+        x[4 + t] = (float)b[t];
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* __restrict__ p, const float (&x)[8]) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 a = {(T)x[0], (T)x[1], (T)x[2], (T)x[3]};
+    const t4 b = {(T)x[4], (T)x[5], (T)x[6], (T)x[7]};
+    *reinterpret_cast<t4*>(p) = a;
+    *reinterpret_cast<t4*>(p + 32) = b;
+}
+
+// The value a cache of element type T holds for x: what a later read returns,
+// so a row attended from registers matches the row attended from memory.
+__device__ __forceinline__ void round8(float (&)[8], const float*) {}
+template <typename T>
+__device__ __forceinline__ void round8(float (&x)[8], const T*) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) x[t] = (float)(T)x[t];
+}
+
 // RoPE on a lane's 8 dims.  Pairs (d, d+1), d even, never straddle a lane:
 // dims 4c..4c+3 are pairs 2c, 2c+1 and dims 32+4c.. are pairs 16+2c, 17+2c.
 __device__ __forceinline__ void rope8(float (&x)[8], const float2* __restrict__ cs_row, int c) {
@@ -164,8 +196,8 @@ __device__ __forceinline__ void attend(const float (&q)[G][kDimsPerLane], State<
 // steps run in the main loop; the one partial step at the end of the range (if
 // any) is loaded and masked after it, so the loop body holds a single copy of
 // the softmax state.
-template <int G, int KVS, int ROW, int NW, int DEPTH>
-__device__ __forceinline__ void attend_rows(const float* __restrict__ kb, const float* __restrict__ vb,
+template <typename T, int G, int KVS, int ROW, int NW, int DEPTH>
+__device__ __forceinline__ void attend_rows(const T* __restrict__ kb, const T* __restrict__ vb,
                                             int n_rows, int wave, int lane_off, int lane_row,
                                             int lane_col, const float (&q)[G][kDimsPerLane], State<G>& st,
                                             int rot, bool blocked) {
@@ -192,8 +224,8 @@ __device__ __forceinline__ void attend_rows(const float* __restrict__ kb, const 
         // ranges (spreads the HBM channels; the merge is order-independent).
         rot %= nk;
         float kbuf[DEPTH][kDimsPerLane], vbuf[DEPTH][kDimsPerLane];
-        const float* kp = kb + (size_t)first * STEP + lane_off;
-        const float* vp = vb + (size_t)first * STEP + lane_off;
+        const T* kp = kb + (size_t)first * STEP + lane_off;
+        const T* vp = vb + (size_t)first * STEP + lane_off;
         auto at = [&](int k) {
             int kk = k + rot;
             kk -= (kk >= nk) ? nk : 0;
@@ -359,7 +391,7 @@ __device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths,
 //   PER_HEAD = true ("head" kernel, short contexts): grid (q head, seq), one
 //     split; the workgroup attends all rows for one query head, reading only
 //     its kv head's 256-byte half rows, so no cross-workgroup merge is needed.
-template <int G, int KV, int NW, int DEPTH, int MODE, bool PER_HEAD>
+template <typename T, int G, int KV, int NW, int DEPTH, int MODE, bool PER_HEAD>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     constexpr int ROW = KV * kHeadDim;
     constexpr int NH = KV * G;
@@ -421,9 +453,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 
     State<GW> st;
     state_init(st);
-    const float* kseq = a.k + base;
-    const float* vseq = a.v + base;
-    attend_rows<GW, KVS, ROW, NW, DEPTH>(kseq + (size_t)r0 * ROW, vseq + (size_t)r0 * ROW, max(r1 - r0, 0),
+    const T* kseq = reinterpret_cast<const T*>(a.k) + base;
+    const T* vseq = reinterpret_cast<const T*>(a.v) + base;
+    attend_rows<T, GW, KVS, ROW, NW, DEPTH>(kseq + (size_t)r0 * ROW, vseq + (size_t)r0 * ROW, max(r1 - r0, 0),
                                          wave, lane_off, lane_row, lane_col, q, st,
                                          (blockIdx.y * gridDim.x + blockIdx.x) * a.rot_mul, a.blocked != 0);
 
@@ -436,9 +468,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
             load8(kf, a.k_new + lane_col);
             load8(vf, a.v_new + lane_col);
             rope8(kf, cs_row, c);
+            round8(kf, kseq);
+            round8(vf, kseq);
             if (!PER_HEAD || head % G == 0) {
-                store8(a.k_out + (size_t)pos * ROW + lane_col, kf);
-                store8(a.v_out + (size_t)pos * ROW + lane_col, vf);
+                store8(reinterpret_cast<T*>(a.k_out) + (size_t)pos * ROW + lane_col, kf);
+                store8(reinterpret_cast<T*>(a.v_out) + (size_t)pos * ROW + lane_col, vf);
             }
         } else {
 #pragma unroll
@@ -461,7 +495,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 // overlaps the K/V traffic.  Every step runs the masked path (rows at or past
 // the length get score -inf and V = 0), so the loop carries one copy of the
 // softmax state and stale rows past the length never reach the sums.
-template <int G, int KV, int NW, int DEPTH, int MODE>
+template <typename T, int G, int KV, int NW, int DEPTH, int MODE>
 __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     constexpr int ROW = KV * kHeadDim;
     constexpr int NH = KV * G;
@@ -495,8 +529,8 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     } else {
         bound = a.capacity;
     }
-    const float* kb = a.k + base + wave * STEP + lane_off;
-    const float* vb = a.v + base + wave * STEP + lane_off;
+    const T* kb = reinterpret_cast<const T*>(a.k) + base + wave * STEP + lane_off;
+    const T* vb = reinterpret_cast<const T*>(a.v) + base + wave * STEP + lane_off;
     auto row_off = [&](int k) {  // float offset (from kb) of this lane's row in the wave's k-th step
         const int row = (wave + NW * k) * PPS + slot;
         const int r = min(row, bound - 1);
@@ -577,9 +611,11 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     if (MODE == kLayer && wave == 0) {
         if (new_lane) {
             rope8(kn, cs_row, c);
+            round8(kn, kb);
+            round8(vn, kb);
             if (head % G == 0) {
-                store8(a.k_out + (size_t)pos * ROW + lane_col, kn);
-                store8(a.v_out + (size_t)pos * ROW + lane_col, vn);
+                store8(reinterpret_cast<T*>(a.k_out) + (size_t)pos * ROW + lane_col, kn);
+                store8(reinterpret_cast<T*>(a.v_out) + (size_t)pos * ROW + lane_col, vn);
             }
         } else {
 #pragma unroll
@@ -645,29 +681,45 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
 #define TMAC_MODE_KERNELS(G, KV, M, MODE)                                                          \
     extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_##M##_g##G##_kv##KV(        \
         DecodeArgs a) {                                                                            \
-        decode_body<G, KV, kGroupWaves, kPrefetchDepth, MODE, false>(a);                           \
+        decode_body<float, G, KV, kGroupWaves, kPrefetchDepth, MODE, false>(a);                       \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(256) void tmac_##M##_g4w_g##G##_kv##KV(DecodeArgs a) {  \
-        decode_body<G, KV, 4, kPrefetchDepth, MODE, false>(a);                                     \
+        decode_body<float, G, KV, 4, kPrefetchDepth, MODE, false>(a);                                 \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(kHeadWaves * 64) void tmac_##M##_head_g##G##_kv##KV(    \
         DecodeArgs a) {                                                                            \
-        head_body<G, KV, kHeadWaves, kHeadPrefetchDepth, MODE>(a);                                 \
+        head_body<float, G, KV, kHeadWaves, kHeadPrefetchDepth, MODE>(a);                           \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(512) void tmac_##M##_head8_g##G##_kv##KV(DecodeArgs a) { \
-        head_body<G, KV, 8, kHeadPrefetchDepth, MODE>(a);                                          \
+        head_body<float, G, KV, 8, kHeadPrefetchDepth, MODE>(a);                                    \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(256) void tmac_##M##_head4_g##G##_kv##KV(DecodeArgs a) { \
-        head_body<G, KV, 4, kHeadPrefetchDepth, MODE>(a);                                          \
+        head_body<float, G, KV, 4, kHeadPrefetchDepth, MODE>(a);                                    \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(64) void tmac_##M##_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, MODE>(a);                                                              \
     }
 
-#define TMAC_DECODE_KERNELS(G, KV)              \
-    TMAC_MODE_KERNELS(G, KV, decode_u, kUniform) \
-    TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)  \
-    TMAC_MODE_KERNELS(G, KV, layer, kLayer)
+// 16-bit caches: the default group (8 waves) and head (8 waves) kernels.
+#define TMAC_MODE_KERNELS16(G, KV, M, MODE, TN, T)                                                     \
+    extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_##M##_##TN##_g##G##_kv##KV(     \
+        DecodeArgs a) {                                                                                \
+        decode_body<T, G, KV, kGroupWaves, kPrefetchDepth, MODE, false>(a);                            \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(512) void tmac_##M##_##TN##_head8_g##G##_kv##KV(DecodeArgs a) { \
+        head_body<T, G, KV, 8, kHeadPrefetchDepth, MODE>(a);                                           \
+    }
+
+#define TMAC_DECODE_KERNELS(G, KV)                           \
+    TMAC_MODE_KERNELS(G, KV, decode_u, kUniform)              \
+    TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)               \
+    TMAC_MODE_KERNELS(G, KV, layer, kLayer)                   \
+    TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, bf16, __bf16) \
+    TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, bf16, __bf16)  \
+    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, bf16, __bf16)      \
+    TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, f16, _Float16) \
+    TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, f16, _Float16)  \
+    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, f16, _Float16)
 
 // (query heads per kv head, kv heads).  Qwen2-0.5B is (7, 2).
 TMAC_DECODE_KERNELS(7, 2)
@@ -1200,6 +1252,16 @@ extern "C" __global__ __launch_bounds__(256) void tmac_rope(RopeArgs a) {
 extern "C" __global__ __launch_bounds__(256) void tmac_copy(CopyArgs a) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.n) a.dst[i] = a.add ? a.dst[i] + a.src[i] : a.src[i];
+}
+
+// Fills a 16-bit cache from fp32 values, rounding to nearest even.
+extern "C" __global__ __launch_bounds__(256) void tmac_cvt16(CvtArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    if (a.dtype == 1)
+        reinterpret_cast<__bf16*>(a.dst)[i] = (__bf16)a.src[i];
+    else
+        reinterpret_cast<_Float16*>(a.dst)[i] = (_Float16)a.src[i];
 }
 
 // Device-side position for graph replays: *pos = value, or *pos += value.

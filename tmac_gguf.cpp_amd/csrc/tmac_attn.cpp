@@ -28,6 +28,7 @@ extern "C" const unsigned char tmac_attn_code_object[];
 extern "C" const uint64_t tmac_attn_code_object_size;
 
 using tmac::CopyArgs;
+using tmac::CvtArgs;
 using tmac::DecodeArgs;
 using tmac::PrefillArgs;
 using tmac::kPrefillKeys;
@@ -76,9 +77,11 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head8[3];    // head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> head4[3];    // head kernel, 4 waves
     std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
+    std::map<std::pair<int, int>, hipFunction_t> decode16[2][3];  // 16-bit caches (bf16, fp16): group kernel
+    std::map<std::pair<int, int>, hipFunction_t> head16[2][3];    // 16-bit caches: head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
-    hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr;
+    hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr;
     float* ws = nullptr;
     size_t ws_floats = 0;
     int* err = nullptr;
@@ -136,8 +139,13 @@ struct Kernels {
     int group_waves = 8;
 };
 
-// Validates the attention shape shared by every decode entry point.
-int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kernels* k, int mode) {
+// Validates the attention shape shared by every decode entry point and picks
+// the kernels for cache element type `dt` (TMAC_KV_F32 / _BF16 / _F16; the
+// 16-bit caches use the default 8-wave group and head kernels).
+int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kernels* k, int mode,
+                int dt = TMAC_KV_F32) {
+    if (dt != TMAC_KV_F32 && dt != TMAC_KV_BF16 && dt != TMAC_KV_F16)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "kv_dtype must be TMAC_KV_F32, TMAC_KV_BF16 or TMAC_KV_F16");
     if (head_dim != kHeadDim)
         return fail(ctx, TMAC_ERR_UNSUPPORTED, "head_dim must be 64 (got " + std::to_string(head_dim) + ")");
     if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head != 0)
@@ -154,6 +162,12 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
         k->head_waves = (int)ctx->opt_head_waves;
         k->head = (k->head_waves == 8 ? ctx->head8 : k->head_waves == 4 ? ctx->head4 : ctx->head)[mode].at({g, n_kv_head});
         k->combine = ctx->combine[mode].at({g, n_kv_head});
+        if (dt != TMAC_KV_F32) {
+            k->group_waves = 8;
+            k->group = ctx->decode16[dt - 1][mode].at({g, n_kv_head});
+            k->head_waves = 8;
+            k->head = ctx->head16[dt - 1][mode].at({g, n_kv_head});
+        }
     }
     return TMAC_OK;
 }
@@ -385,6 +399,17 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->decode[m][{sh[0], sh[1]}] = f;
+            for (int dt = 0; dt < 2; dt++) {
+                const char* tn = dt == 0 ? "bf16" : "f16";
+                std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mode_prefix[m], tn, sh[0], sh[1]);
+                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                    return bail(hip_fail(ctx, e, name));
+                ctx->decode16[dt][m][{sh[0], sh[1]}] = f;
+                std::snprintf(name, sizeof(name), "%s_%s_head8_g%d_kv%d", mode_prefix[m], tn, sh[0], sh[1]);
+                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                    return bail(hip_fail(ctx, e, name));
+                ctx->head16[dt][m][{sh[0], sh[1]}] = f;
+            }
             std::snprintf(name, sizeof(name), "%s_g4w_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
@@ -422,7 +447,8 @@ int tmac_init(tmac_context** out, int device) {
     if ((e = hipModuleGetFunction(&ctx->k_rope, ctx->module, "tmac_rope")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->k_copy, ctx->module, "tmac_copy")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->k_pos, ctx->module, "tmac_pos_update")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_qkv, ctx->module, "tmac_qkv")) != hipSuccess)
+        (e = hipModuleGetFunction(&ctx->k_qkv, ctx->module, "tmac_qkv")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->k_cvt16, ctx->module, "tmac_cvt16")) != hipSuccess)
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
@@ -469,24 +495,24 @@ int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, con
     return run_decode(ctx, (hipStream_t)stream, kern, a, 1, past_len + 1, n_kv_head);
 }
 
-int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const float* q, const float* k,
-                                  const float* v, float* out, int n_seq, int n_head, int n_kv_head,
-                                  int head_dim, int n_pos, int64_t seq_stride) {
+static int decode_batched_impl(tmac_context* ctx, tmac_stream stream, int dt, const float* q, const void* k,
+                               const void* v, float* out, int n_seq, int n_head, int n_kv_head, int head_dim,
+                               int n_pos, int64_t seq_stride) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if (!q || !k || !v || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "decode_batched: null buffer");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "decode_batched: buffers must be 16-byte aligned");
     Kernels kern;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeUniform))) return rc;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeUniform, dt))) return rc;
     if (n_seq < 0 || n_pos < 1 || seq_stride < 0 || (n_seq > 1 && seq_stride < n_pos))
         return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_batched: need n_seq >= 0, n_pos >= 1, seq_stride >= n_pos");
     if (n_seq == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
     DecodeArgs a{};
     a.q = q;
-    a.k = k;
-    a.v = v;
+    a.k = static_cast<const float*>(k);
+    a.v = static_cast<const float*>(v);
     a.out = out;
     a.seq_stride = seq_stride;
     a.n_pos = n_pos;
@@ -494,10 +520,23 @@ int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const f
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, n_pos, n_kv_head);
 }
 
-int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const float* q,
-                                 const float* k_pool, const float* v_pool, const int64_t* offsets,
-                                 const int32_t* lengths, float* out, int n_seq, int n_head,
-                                 int n_kv_head, int head_dim, int max_len, int64_t total_rows) {
+int tmac_attention_decode_batched(tmac_context* ctx, tmac_stream stream, const float* q, const float* k,
+                                  const float* v, float* out, int n_seq, int n_head, int n_kv_head,
+                                  int head_dim, int n_pos, int64_t seq_stride) {
+    return decode_batched_impl(ctx, stream, TMAC_KV_F32, q, k, v, out, n_seq, n_head, n_kv_head, head_dim, n_pos,
+                               seq_stride);
+}
+
+int tmac_attention_decode_batched_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                     const void* k, const void* v, float* out, int n_seq, int n_head,
+                                     int n_kv_head, int head_dim, int n_pos, int64_t seq_stride) {
+    return decode_batched_impl(ctx, stream, kv_dtype, q, k, v, out, n_seq, n_head, n_kv_head, head_dim, n_pos,
+                               seq_stride);
+}
+
+static int decode_ragged_impl(tmac_context* ctx, tmac_stream stream, int dt, const float* q, const void* k_pool,
+                              const void* v_pool, const int64_t* offsets, const int32_t* lengths, float* out,
+                              int n_seq, int n_head, int n_kv_head, int head_dim, int max_len, int64_t total_rows) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if (!q || !k_pool || !v_pool || !offsets || !lengths || !out)
@@ -505,15 +544,15 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
     if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "decode_ragged: buffers must be 16-byte aligned");
     Kernels kern;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeRagged))) return rc;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeRagged, dt))) return rc;
     if (n_seq < 0 || max_len < 1 || total_rows < 0)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: need max_len >= 1, total_rows >= 0");
     if (n_seq == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
     DecodeArgs a{};
     a.q = q;
-    a.k = k_pool;
-    a.v = v_pool;
+    a.k = static_cast<const float*>(k_pool);
+    a.v = static_cast<const float*>(v_pool);
     a.out = out;
     a.offsets = offsets;
     a.lengths = lengths;
@@ -521,10 +560,26 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head, total_rows);
 }
 
+int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const float* q,
+                                 const float* k_pool, const float* v_pool, const int64_t* offsets,
+                                 const int32_t* lengths, float* out, int n_seq, int n_head,
+                                 int n_kv_head, int head_dim, int max_len, int64_t total_rows) {
+    return decode_ragged_impl(ctx, stream, TMAC_KV_F32, q, k_pool, v_pool, offsets, lengths, out, n_seq, n_head,
+                              n_kv_head, head_dim, max_len, total_rows);
+}
+
+int tmac_attention_decode_ragged_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                    const void* k_pool, const void* v_pool, const int64_t* offsets,
+                                    const int32_t* lengths, float* out, int n_seq, int n_head, int n_kv_head,
+                                    int head_dim, int max_len, int64_t total_rows) {
+    return decode_ragged_impl(ctx, stream, kv_dtype, q, k_pool, v_pool, offsets, lengths, out, n_seq, n_head,
+                              n_kv_head, head_dim, max_len, total_rows);
+}
+
 static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, const float* k_new,
-                        const float* v_new, float* k_cache, float* v_cache, float* out, int n_head,
+                        const float* v_new, void* k_cache, void* v_cache, float* out, int n_head,
                         int n_kv_head, int head_dim, int pos, const int* pos_dev, int capacity,
-                        float base) {
+                        float base, int dt = TMAC_KV_F32) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if (!q || !k_new || !v_new || !k_cache || !v_cache || !out)
@@ -533,7 +588,7 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
         !aligned16(v_cache) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "layer_attention: buffers must be 16-byte aligned");
     Kernels kern;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeLayer))) return rc;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeLayer, dt))) return rc;
     if (capacity < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "layer_attention: capacity < 1");
     if (!pos_dev && (pos < 0 || pos >= capacity))
         return fail(ctx, TMAC_ERR_CAPACITY, "layer_attention: pos outside [0, capacity)");
@@ -543,14 +598,14 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
     if ((rc = rope_table(ctx, stream, head_dim, base, pos_dev ? capacity : pos + 1, &rt))) return rc;
     DecodeArgs a{};
     a.q = q;
-    a.k = k_cache;
-    a.v = v_cache;
+    a.k = static_cast<const float*>(k_cache);
+    a.v = static_cast<const float*>(v_cache);
     a.out = out;
     a.n_head = n_head;
     a.k_new = k_new;
     a.v_new = v_new;
-    a.k_out = k_cache;
-    a.v_out = v_cache;
+    a.k_out = static_cast<float*>(k_cache);
+    a.v_out = static_cast<float*>(v_cache);
     a.rope_cs = rt->dev;
     a.rope_rows = rt->rows;
     a.pos_dev = pos_dev;
@@ -570,9 +625,43 @@ int tmac_layer_attention_devpos(tmac_context* ctx, tmac_stream stream, const flo
                                 const float* k_new, const float* v_new, float* k_cache,
                                 float* v_cache, float* out, int n_head, int n_kv_head, int head_dim,
                                 const int* pos_dev, int capacity, float base) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
     if (!pos_dev) return fail(ctx, TMAC_ERR_NULL_POINTER, "layer_attention_devpos: null pos_dev");
     return layer_common(ctx, (hipStream_t)stream, q, k_new, v_new, k_cache, v_cache, out, n_head,
                         n_kv_head, head_dim, 0, pos_dev, capacity, base);
+}
+
+int tmac_layer_attention_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                            const float* k_new, const float* v_new, void* k_cache, void* v_cache, float* out,
+                            int n_head, int n_kv_head, int head_dim, int pos, int capacity, float base) {
+    return layer_common(ctx, (hipStream_t)stream, q, k_new, v_new, k_cache, v_cache, out, n_head, n_kv_head,
+                        head_dim, pos, nullptr, capacity, base, kv_dtype);
+}
+
+int tmac_layer_attention_devpos_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                   const float* k_new, const float* v_new, void* k_cache, void* v_cache,
+                                   float* out, int n_head, int n_kv_head, int head_dim, const int* pos_dev,
+                                   int capacity, float base) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!pos_dev) return fail(ctx, TMAC_ERR_NULL_POINTER, "layer_attention_devpos: null pos_dev");
+    return layer_common(ctx, (hipStream_t)stream, q, k_new, v_new, k_cache, v_cache, out, n_head, n_kv_head,
+                        head_dim, 0, pos_dev, capacity, base, kv_dtype);
+}
+
+int tmac_kv_convert(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* src, void* dst, int64_t n) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (kv_dtype != TMAC_KV_BF16 && kv_dtype != TMAC_KV_F16)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "kv_convert: kv_dtype must be TMAC_KV_BF16 or TMAC_KV_F16");
+    if (!src || !dst) return fail(ctx, TMAC_ERR_NULL_POINTER, "kv_convert: null buffer");
+    if (n < 0 || (n + 255) / 256 > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "kv_convert: bad count");
+    if (((uintptr_t)src % 4) || ((uintptr_t)dst % 2)) return fail(ctx, TMAC_ERR_MISALIGNED, "kv_convert: misaligned");
+    if (n == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    CvtArgs a{src, dst, n, kv_dtype};
+    return launch(ctx, ctx->k_cvt16, (unsigned)((n + 255) / 256), 1, 256, (hipStream_t)stream, &a);
 }
 
 int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,

@@ -34,6 +34,9 @@ TMAC_ERR_HIP_BASE = 1000
 
 TMAC_Q5_0 = 6
 TMAC_Q8_0 = 8
+TMAC_KV_F32 = 0
+TMAC_KV_BF16 = 1
+TMAC_KV_F16 = 2
 TMAC_OPT_SPLIT_LEN = 1
 TMAC_OPT_TARGET_GROUPS = 2
 TMAC_OPT_KERNEL = 3
@@ -63,6 +66,13 @@ SIGNATURES = {
     "tmac_elem_op": (_i, [_vp, _vp, _i, _vp, _vp, _i]),
     "tmac_fused_qkv_op": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "tmac_fused_qkv_bias": (_i, [_vp] * 12 + [_i] * 5),
+    "tmac_attention_decode_batched_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
+    "tmac_attention_decode_ragged_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                             _i64]),
+    "tmac_layer_attention_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f]),
+    "tmac_layer_attention_devpos_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i,
+                                            _f]),
+    "tmac_kv_convert": (_i, [_vp, _vp, _i, _vp, _vp, _i64]),
     "tmac_matmul_q8_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "tmac_matmul_q5_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "tmac_matmul_add": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
@@ -318,19 +328,30 @@ class Context:
         return rc
 
     def layer_attention(self, q, k_new, v_new, k_cache, v_cache, out, n_head, n_kv_head, head_dim,
-                        pos, capacity, base=1e6, stream=None, check=True) -> int:
-        rc = self.lib.tmac_layer_attention(self.handle, stream, _p(q), _p(k_new), _p(v_new),
-                                           _p(k_cache), _p(v_cache), _p(out), n_head, n_kv_head,
-                                           head_dim, pos, capacity, base)
+                        pos, capacity, base=1e6, stream=None, check=True, kv_dtype=TMAC_KV_F32) -> int:
+        if kv_dtype == TMAC_KV_F32:
+            rc = self.lib.tmac_layer_attention(self.handle, stream, _p(q), _p(k_new), _p(v_new),
+                                               _p(k_cache), _p(v_cache), _p(out), n_head, n_kv_head,
+                                               head_dim, pos, capacity, base)
+        else:
+            rc = self.lib.tmac_layer_attention_kv(self.handle, stream, kv_dtype, _p(q), _p(k_new), _p(v_new),
+                                                  _p(k_cache), _p(v_cache), _p(out), n_head, n_kv_head,
+                                                  head_dim, pos, capacity, base)
         if check:
             self._check(rc, "layer_attention")
         return rc
 
     def layer_attention_devpos(self, q, k_new, v_new, k_cache, v_cache, out, n_head, n_kv_head,
-                               head_dim, pos_dev, capacity, base=1e6, stream=None, check=True) -> int:
-        rc = self.lib.tmac_layer_attention_devpos(self.handle, stream, _p(q), _p(k_new), _p(v_new),
-                                                  _p(k_cache), _p(v_cache), _p(out), n_head,
-                                                  n_kv_head, head_dim, _p(pos_dev), capacity, base)
+                               head_dim, pos_dev, capacity, base=1e6, stream=None, check=True,
+                               kv_dtype=TMAC_KV_F32) -> int:
+        if kv_dtype == TMAC_KV_F32:
+            rc = self.lib.tmac_layer_attention_devpos(self.handle, stream, _p(q), _p(k_new), _p(v_new),
+                                                      _p(k_cache), _p(v_cache), _p(out), n_head,
+                                                      n_kv_head, head_dim, _p(pos_dev), capacity, base)
+        else:
+            rc = self.lib.tmac_layer_attention_devpos_kv(self.handle, stream, kv_dtype, _p(q), _p(k_new),
+                                                         _p(v_new), _p(k_cache), _p(v_cache), _p(out), n_head,
+                                                         n_kv_head, head_dim, _p(pos_dev), capacity, base)
         if check:
             self._check(rc, "layer_attention_devpos")
         return rc
@@ -343,20 +364,36 @@ class Context:
         self._check(self.lib.tmac_rope_prepare(self.handle, head_dim, base, n_pos), "rope_prepare")
 
     def decode_batched(self, q, k, v, out, n_seq, n_head, n_kv_head, head_dim, n_pos, seq_stride,
-                       stream=None, check=True) -> int:
-        rc = self.lib.tmac_attention_decode_batched(self.handle, stream, _p(q), _p(k), _p(v), _p(out),
-                                                    n_seq, n_head, n_kv_head, head_dim, n_pos, seq_stride)
+                       stream=None, check=True, kv_dtype=TMAC_KV_F32) -> int:
+        if kv_dtype == TMAC_KV_F32:
+            rc = self.lib.tmac_attention_decode_batched(self.handle, stream, _p(q), _p(k), _p(v), _p(out),
+                                                        n_seq, n_head, n_kv_head, head_dim, n_pos, seq_stride)
+        else:
+            rc = self.lib.tmac_attention_decode_batched_kv(self.handle, stream, kv_dtype, _p(q), _p(k), _p(v),
+                                                           _p(out), n_seq, n_head, n_kv_head, head_dim, n_pos,
+                                                           seq_stride)
         if check:
             self._check(rc, "decode_batched")
         return rc
 
     def decode_ragged(self, q, k_pool, v_pool, offsets, lengths, out, n_seq, n_head, n_kv_head,
-                      head_dim, max_len, total_rows=0, stream=None, check=True) -> int:
-        rc = self.lib.tmac_attention_decode_ragged(self.handle, stream, _p(q), _p(k_pool), _p(v_pool),
-                                                   _p(offsets), _p(lengths), _p(out), n_seq, n_head,
-                                                   n_kv_head, head_dim, max_len, total_rows)
+                      head_dim, max_len, total_rows=0, stream=None, check=True, kv_dtype=TMAC_KV_F32) -> int:
+        if kv_dtype == TMAC_KV_F32:
+            rc = self.lib.tmac_attention_decode_ragged(self.handle, stream, _p(q), _p(k_pool), _p(v_pool),
+                                                       _p(offsets), _p(lengths), _p(out), n_seq, n_head,
+                                                       n_kv_head, head_dim, max_len, total_rows)
+        else:
+            rc = self.lib.tmac_attention_decode_ragged_kv(self.handle, stream, kv_dtype, _p(q), _p(k_pool),
+                                                          _p(v_pool), _p(offsets), _p(lengths), _p(out), n_seq,
+                                                          n_head, n_kv_head, head_dim, max_len, total_rows)
         if check:
             self._check(rc, "decode_ragged")
+        return rc
+
+    def kv_convert(self, kv_dtype, src, dst, n, stream=None, check=True) -> int:
+        rc = self.lib.tmac_kv_convert(self.handle, stream, kv_dtype, _p(src), _p(dst), n)
+        if check:
+            self._check(rc, "kv_convert")
         return rc
 
     def prefill(self, q, k, v, out, n_seq, n_q, prefix_len, seq_stride, n_head, n_kv_head, head_dim,
