@@ -10,7 +10,8 @@ namespace tmac {
 constexpr int kHeadDim = 64;        // the reference's flash kernel supports only 64 (kernel_flash_attn.metal:18)
 constexpr int kSlotsPerWave = 8;    // 64 lanes = 8 (row, kv-head) slots x 8 dim-lanes
 constexpr int kGroupWaves = 8;      // "group" decode kernel: 512 threads per workgroup
-constexpr int kPrefetchDepth = 3;   // group kernel: steps of K/V in flight per wave (242 VGPRs at G = 7)
+constexpr int kPrefetchDepth = 3;   // group kernel: steps of K/V in flight per wave (191 VGPRs at G = 7)
+constexpr int kPrefetchDepth16 = 6; // the same for 16-bit caches: half the bytes per step, twice the steps
 constexpr int kHeadWaves = 16;      // "head" decode kernel (short contexts): 1024 threads
 constexpr int kHeadPrefetchDepth = 2;
 constexpr int kMaxSplits = 256;     // split-KV workgroups per sequence, at most

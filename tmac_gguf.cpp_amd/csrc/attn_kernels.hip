@@ -704,7 +704,7 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
 #define TMAC_MODE_KERNELS16(G, KV, M, MODE, TN, T)                                                     \
     extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_##M##_##TN##_g##G##_kv##KV(     \
         DecodeArgs a) {                                                                                \
-        decode_body<T, G, KV, kGroupWaves, kPrefetchDepth, MODE, false>(a);                            \
+        decode_body<T, G, KV, kGroupWaves, kPrefetchDepth16, MODE, false>(a);                          \
     }                                                                                                  \
     extern "C" __global__ __launch_bounds__(512) void tmac_##M##_##TN##_head8_g##G##_kv##KV(DecodeArgs a) { \
         head_body<T, G, KV, 8, kHeadPrefetchDepth, MODE>(a);                                           \
