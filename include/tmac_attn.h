@@ -121,10 +121,19 @@ int tmac_fused_qkv_bias(tmac_context* ctx, tmac_stream stream, const void* w_q, 
  * the engine calls them through matmul() (tmac_gguf.cpp:476-490) for
  * attn_output.weight (tmac_gguf.cpp:1497-1498).  y = W x, W rows x cols in
  * Q8_0 / Q5_0 blocks as above; x 16-byte aligned, x and y disjoint. */
-enum tmac_weight_type { TMAC_Q5_0 = 6, TMAC_Q8_0 = 8 };  /* the reference's tensor type codes (tmac_gguf.cpp:179-181) */
+/* the reference's tensor type codes (tmac_gguf.cpp:176-182) */
+enum tmac_weight_type { TMAC_F32 = 0, TMAC_F16 = 1, TMAC_Q5_0 = 6, TMAC_Q8_0 = 8, TMAC_Q4_K = 12, TMAC_Q6_K = 14 };
 int tmac_matmul_q8_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
                      float* y);
 int tmac_matmul_q5_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y);
+/* matmul_q4_k / matmul_q6_k, metal_backend.hpp:340-350: K-quant super-blocks of
+ * 256 weights along a row (Q4_K 144 bytes: fp16 d, fp16 dmin, 12 bytes of
+ * 6-bit scales/mins, 128 bytes of nibbles; Q6_K 210 bytes: ql[128], qh[64],
+ * int8 scales[16], fp16 d; tmac_gguf.cpp:330-397).  cols a multiple of 256. */
+int tmac_matmul_q4_k(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y);
+int tmac_matmul_q6_k(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
                      float* y);
 /* Extension: y += W x in one launch, i.e. the projection followed by the
  * residual add elem_op(0, hidden, attn_out) (tmac_gguf.cpp:1497-1499):

@@ -12,6 +12,7 @@
 //   metal_backend::fused_qkv_op(ctx, Wq, Wk, Wv, x, q, k, v, ...)       :456-489
 //   metal_backend::elem_op(ctx, 0, q|k|v, bias, dim)  (bias adds, tmac_gguf.cpp:1484-1489)
 //   metal_backend::matmul_q5_0 / matmul_q8_0(ctx, rows, cols, W, x, y)   :320-338
+//   metal_backend::matmul_q4_k / matmul_q6_k(ctx, rows, cols, W, x, y)   :340-350
 //   metal_backend::elem_op(ctx, 0, hidden, attn_out, dim)  (residual, tmac_gguf.cpp:1499)
 //   metal_backend::attention_op(ctx, Q, K, V, out, n_head, n_kv_head, head_dim, past_len) :413-453
 //   metal_backend::metal_batch_end()                 metal_backend.hpp:176-190
@@ -136,6 +137,14 @@ inline void matmul_q8_0(Context& c, int rows, int cols, const uint8_t* w, const 
 
 inline void matmul_q5_0(Context& c, int rows, int cols, const uint8_t* w, const float* x, float* y) {
     detail::note(c, tmac_matmul_q5_0(c.ctx, c.stream, rows, cols, w, x, y), "matmul_q5_0");
+}
+
+inline void matmul_q4_k(Context& c, int rows, int cols, const uint8_t* w, const float* x, float* y) {
+    detail::note(c, tmac_matmul_q4_k(c.ctx, c.stream, rows, cols, w, x, y), "matmul_q4_k");
+}
+
+inline void matmul_q6_k(Context& c, int rows, int cols, const uint8_t* w, const float* x, float* y) {
+    detail::note(c, tmac_matmul_q6_k(c.ctx, c.stream, rows, cols, w, x, y), "matmul_q6_k");
 }
 
 // y += W x: the output projection and the residual add in one launch.

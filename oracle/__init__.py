@@ -210,8 +210,9 @@ def max_threads(timing: bool = False) -> int:
 
 
 # ---- quantized weights (tmac_gguf.cpp:219-231, 240-250, 311-327, 510-514, 1046-1081) ----
-Q5_0, Q8_0 = 6, 8
-BLOCK_BYTES = {Q5_0: 22, Q8_0: 34}
+Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
+BLOCK_BYTES = {Q5_0: 22, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+BLOCK_ELEMS = {Q5_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
 
 
 def _u8(a) -> np.ndarray:
@@ -233,7 +234,7 @@ def matmul_q(qtype: int, w, x, rows: int, cols: int) -> np.ndarray:
     rows of cols/32 blocks of `qtype`."""
     w = _u8(w)
     x = _f32(x)
-    if w.size < rows * (cols // 32) * BLOCK_BYTES.get(qtype, 0) or x.size < cols:
+    if w.size < rows * (cols // BLOCK_ELEMS.get(qtype, 32)) * BLOCK_BYTES.get(qtype, 0) or x.size < cols:
         raise ValueError("matmul_q: buffers too small")
     y = np.empty(rows, dtype=np.float32)
     if lib().oracle_matmul_q(qtype, w.ctypes.data, _fp(x), _fp(y), rows, cols) != 0:

@@ -303,8 +303,49 @@ float oracle_f16_to_f32(uint16_t f16) {
     return (sign ? -1.0f : 1.0f) * (1.0f + mant / 1024.0f) * powf(2.0f, (int)ex - 15);
 }
 
-/* tmac_gguf.cpp:240-250 (Q8_0) and 311-327 (Q5_0): the weight at flat index idx. */
+/* tmac_gguf.cpp:330-366: element (half, sub, l) of a 210-byte super-block:
+ * 4 low bits from ql (sub 0/2: bytes l, sub 1/3: bytes l + 32, low nibble for
+ * sub 0/1, high for 2/3), 2 high bits from qh byte l at shift 2*sub, minus 32;
+ * times the int8 scale l / 16 + 2*sub and d, multiplied in that order. */
+static float dequant_q6_k(const uint8_t* data, uint64_t idx) {
+    const uint64_t block = idx / 256, offset = idx % 256, base = block * 210;
+    const float d = oracle_f16_to_f32((uint16_t)(data[base + 208] | (data[base + 209] << 8)));
+    const uint64_t half = offset / 128, pos = offset % 128, l = pos % 32, sub = pos / 32;
+    const uint64_t ql_base = base + half * 64, qh_base = base + 128 + half * 32, sc_base = base + 192 + half * 8;
+    const uint8_t ql_byte = data[ql_base + l + ((sub & 1) ? 32 : 0)];
+    const uint8_t ql = (sub < 2) ? (ql_byte & 0xF) : (ql_byte >> 4);
+    const uint8_t qh = (data[qh_base + l] >> (2 * sub)) & 0x3;
+    const int8_t q = (int8_t)((qh << 4) | ql) - 32;
+    const int8_t scale = (int8_t)data[sc_base + l / 16 + sub * 2];
+    return d * scale * q;
+}
+
+/* tmac_gguf.cpp:368-397: sub-block sb = e / 32 of a 144-byte super-block;
+ * nibble of qs[(sb / 2) * 32 + e % 32] (low for even sb); 6-bit scale and min
+ * unpacked from the 12 scale bytes; w = d * sc * q - dmin * m. */
+static float dequant_q4_k(const uint8_t* data, uint64_t idx) {
+    const uint64_t block = idx / 256, offset = idx % 256, base = block * 144;
+    const float d = oracle_f16_to_f32((uint16_t)(data[base] | (data[base + 1] << 8)));
+    const float dmin = oracle_f16_to_f32((uint16_t)(data[base + 2] | (data[base + 3] << 8)));
+    const uint64_t sb = offset / 32, q_pos = offset % 32;
+    const uint8_t qs_byte = data[base + 16 + (sb / 2) * 32 + q_pos];
+    const uint8_t q4 = (sb % 2 == 0) ? (qs_byte & 0xF) : (qs_byte >> 4);
+    const uint8_t* sc6 = data + base + 4;
+    uint8_t sc, m;
+    if (sb < 4) {
+        sc = sc6[sb] & 63;
+        m = sc6[sb + 4] & 63;
+    } else {
+        sc = (sc6[sb + 4] & 0xF) | ((sc6[sb - 4] >> 6) << 4);
+        m = (sc6[sb + 4] >> 4) | ((sc6[sb] >> 6) << 4);
+    }
+    return d * (float)sc * (float)q4 - dmin * (float)m;
+}
+
+/* tmac_gguf.cpp:240-250 (Q8_0), 311-327 (Q5_0), 330-397 (Q6_K, Q4_K): the weight at flat index idx. */
 float oracle_dequant(int type, const uint8_t* data, uint64_t idx) {
+    if (type == ORACLE_Q6_K) return dequant_q6_k(data, idx);
+    if (type == ORACLE_Q4_K) return dequant_q4_k(data, idx);
     const uint64_t block = idx / 32, e = idx % 32;
     if (type == ORACLE_Q8_0) {
         const uint8_t* b = data + block * 34;
@@ -324,7 +365,9 @@ float oracle_dequant(int type, const uint8_t* data, uint64_t idx) {
  * order, the product rounded before the add (no contraction in this build).
  * read_tensor's flat index is col + row * cols (tmac_gguf.cpp:405). */
 int oracle_matmul_q(int type, const uint8_t* w, const float* x, float* y, int rows, int cols) {
-    if (!w || !x || !y || rows < 0 || cols <= 0 || cols % 32 || (type != ORACLE_Q5_0 && type != ORACLE_Q8_0))
+    const int kquant = (type == ORACLE_Q4_K || type == ORACLE_Q6_K);
+    if (!w || !x || !y || rows < 0 || cols <= 0 || cols % (kquant ? 256 : 32) ||
+        (type != ORACLE_Q5_0 && type != ORACLE_Q8_0 && !kquant))
         return -1;
     for (int i = 0; i < rows; i++) {
         float sum = 0;

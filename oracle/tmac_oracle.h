@@ -14,6 +14,7 @@
  *   constants     tmac_gguf.cpp:163-172    (Qwen2-0.5B: 14 q heads, 2 kv heads, head_dim 64)
  *   fp16 decode   tmac_gguf.cpp:219-231    (f16_to_f32)
  *   Q8_0 / Q5_0   tmac_gguf.cpp:240-250, 311-327 (dequant_q8_0 / dequant_q5_0)
+ *   Q6_K / Q4_K   tmac_gguf.cpp:330-397    (dequant_q6_k / dequant_q4_k)
  *   matmul        tmac_gguf.cpp:405-414, 510-514 (read_tensor + the CPU row loop)
  *   QKV + bias    tmac_gguf.cpp:1046-1081  (three matmuls on the normed hidden state, then bias adds)
  *
@@ -102,7 +103,10 @@ int oracle_max_threads(void);
  *   Q5_0 (type 6): fp16 d, uint32 qh, uint8 qs[16]             22 bytes;
  *                  element e: low nibble of qs[e] (e < 16) or high nibble of
  *                  qs[e - 16], fifth bit = bit e of qh, w = d * (q5 - 16)     */
-enum { ORACLE_Q5_0 = 6, ORACLE_Q8_0 = 8 };
+enum { ORACLE_Q5_0 = 6, ORACLE_Q8_0 = 8, ORACLE_Q4_K = 12, ORACLE_Q6_K = 14 };
+/* Super-blocks of 256 weights (cols a multiple of 256):
+ *   Q6_K (type 14): ql[128], qh[64], int8 scales[16], fp16 d              210 bytes
+ *   Q4_K (type 12): fp16 d, fp16 dmin, scales[12] (6-bit sc/m), qs[128]   144 bytes  */
 float oracle_f16_to_f32(uint16_t h);
 float oracle_dequant(int type, const uint8_t* data, uint64_t idx);
 /* y[i] = sum over j ascending of w[i][j] * x[j], one fp32 accumulator per row. */

@@ -177,3 +177,74 @@ def test_output_projection_and_residual(ctx, qtype):
     assert ctx.matmul(7, n, n, dw, dx, dy, accumulate=True, check=False) == tmac_attn.TMAC_ERR_UNSUPPORTED
     for d in (dw, dx, dy, dh, dh2):
         d.free()
+
+
+def kquant_integer_blocks(rng, qtype, n):
+    """Super-blocks whose weights are small integers (d = 1, unit scales), so
+    integer inputs give exact sums in any order."""
+    raw = rng.integers(0, 256, (n, oracle.BLOCK_BYTES[qtype]), dtype=np.uint8)
+    one = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+    if qtype == oracle.Q6_K:
+        raw[:, 208:210] = one
+        raw[:, 192:208] = rng.integers(1, 4, (n, 16))  # int8 scales 1..3
+    else:
+        raw[:, 0:2] = one
+        raw[:, 2:4] = one
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("qtype", [oracle.Q6_K, oracle.Q4_K])
+@pytest.mark.parametrize("rows,cols", [(7, 256), (64, 4864), (129, 1024)])
+def test_kquant_integer_pattern_bit_exact(ctx, qtype, rows, cols):
+    rng = np.random.default_rng(120 + qtype + rows)
+    w = kquant_integer_blocks(rng, qtype, rows * cols // 256)
+    x = np.array([i % 7 - 3 for i in range(cols)], dtype=np.float32)
+    dw, dx, dy = ctx.upload(w), ctx.upload(x), ctx.empty(rows)
+    ctx.matmul(qtype, rows, cols, dw, dx, dy)
+    np.testing.assert_array_equal(dy.numpy(), oracle.matmul_q(qtype, w, x, rows, cols))
+    for d in (dw, dx, dy):
+        d.free()
+
+
+@pytest.mark.parametrize("qtype", [oracle.Q6_K, oracle.Q4_K])
+def test_kquant_matmul_and_residual_match_oracle(ctx, qtype):
+    """ffn_down shape (896 x 4864) with realistic scales; y = W x and y += W x."""
+    rng = np.random.default_rng(130 + qtype)
+    rows, cols = 896, 4864
+    raw = rng.integers(0, 256, (rows * cols // 256, oracle.BLOCK_BYTES[qtype]), dtype=np.uint8)
+    n = raw.shape[0]
+    # super-block scales of a real checkpoint: d * sc (or d * scale) ~ 1e-3 .. 4e-3, |w| ~ 0.03
+    sc = rng.uniform(2e-5, 6e-5, (n, 2)).astype(np.float16)
+    if qtype == oracle.Q6_K:
+        raw[:, 208:210] = sc[:, :1].view(np.uint8).reshape(n, 2)
+    else:
+        raw[:, 0:4] = sc.view(np.uint8).reshape(n, 4)
+    w = raw.reshape(-1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    h = rng.standard_normal(rows).astype(np.float32)
+    ref = oracle.matmul_q(qtype, w, x, rows, cols)
+    dw, dx, dy, dh = ctx.upload(w), ctx.upload(x), ctx.empty(rows), ctx.upload(h)
+    ctx.matmul(qtype, rows, cols, dw, dx, dy)
+    assert_close(dy.numpy(), ref, f"matmul type {qtype}")
+    big = oracle.BLOCK_BYTES[qtype]
+    wl = w.reshape(-1, big).copy()  # the same rows at 40x the scale: the order-independent bound
+    sl = (sc.astype(np.float32) * 40).astype(np.float16)
+    if qtype == oracle.Q6_K:
+        wl[:, 208:210] = sl[:, :1].view(np.uint8).reshape(n, 2)
+    else:
+        wl[:, 0:4] = sl.view(np.uint8).reshape(n, 4)
+    wl = wl.reshape(-1)
+    dwl = ctx.upload(wl)
+    ctx.matmul(qtype, rows, cols, dwl, dx, dy)
+    refl = oracle.matmul_q(qtype, wl, x, rows, cols).astype(np.float64)
+    wabs = np.stack([np.abs(np.array([oracle.dequant(qtype, wl, r * cols + c) for c in range(cols)]))
+                     for r in range(0, rows, 97)])
+    bound = 2 * (cols + 1) * 2.0 ** -24 * (wabs @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(dy.numpy().astype(np.float64)[::97] - refl[::97]) <= bound)
+    dwl.free()
+    ctx.matmul(qtype, rows, cols, dw, dx, dy)
+    ctx.matmul(qtype, rows, cols, dw, dx, dh, accumulate=True)
+    np.testing.assert_array_equal(dh.numpy(), h + dy.numpy())
+    assert ctx.matmul(qtype, rows, 896, dw, dx, dy, check=False) == tmac_attn.TMAC_ERR_INVALID_ARG
+    for d in (dw, dx, dy, dh):
+        d.free()

@@ -168,3 +168,112 @@ def test_qkv_adds_present_biases_only():
     np.testing.assert_array_equal(v, oracle.matmul_q(oracle.Q8_0, wv, x, nv, cols) + bv)
     with pytest.raises(ValueError):
         oracle.matmul_q(oracle.Q5_0, wq, x, nq, 100)
+
+
+# ---- K-quants (tmac_gguf.cpp:330-397), pinned against decoders written from
+# GGML's published row dequantisation loops (dequantize_row_q6_K /
+# dequantize_row_q4_K: per-128 / per-64-element chunks, get_scale_min_k4),
+# whose loop structure differs from the reference's per-element form.
+
+def ggml_q6_k_row(blk: np.ndarray) -> np.ndarray:
+    ql, qh = blk[0:128].astype(np.int64), blk[128:192].astype(np.int64)
+    sc = blk[192:208].view(np.int8).astype(np.float64)
+    d = float(blk[208:210].copy().view(np.float16)[0])
+    y = np.empty(256)
+    for n in range(2):
+        qln, qhn, scn = ql[64 * n:64 * n + 64], qh[32 * n:32 * n + 32], sc[8 * n:8 * n + 8]
+        for l in range(32):
+            is_ = l // 16
+            q1 = ((qln[l] & 0xF) | (((qhn[l] >> 0) & 3) << 4)) - 32
+            q2 = ((qln[l + 32] & 0xF) | (((qhn[l] >> 2) & 3) << 4)) - 32
+            q3 = ((qln[l] >> 4) | (((qhn[l] >> 4) & 3) << 4)) - 32
+            q4 = ((qln[l + 32] >> 4) | (((qhn[l] >> 6) & 3) << 4)) - 32
+            y[128 * n + l + 0] = d * scn[is_ + 0] * q1
+            y[128 * n + l + 32] = d * scn[is_ + 2] * q2
+            y[128 * n + l + 64] = d * scn[is_ + 4] * q3
+            y[128 * n + l + 96] = d * scn[is_ + 6] * q4
+    return y
+
+
+def get_scale_min_k4(j: int, q: np.ndarray):
+    if j < 4:
+        return int(q[j]) & 63, int(q[j + 4]) & 63
+    return (int(q[j + 4]) & 0xF) | ((int(q[j - 4]) >> 6) << 4), (int(q[j + 4]) >> 4) | ((int(q[j]) >> 6) << 4)
+
+
+def ggml_q4_k_row(blk: np.ndarray) -> np.ndarray:
+    d = float(blk[0:2].copy().view(np.float16)[0])
+    dmin = float(blk[2:4].copy().view(np.float16)[0])
+    scales, q = blk[4:16], blk[16:144].astype(np.int64)
+    y = np.empty(256)
+    is_ = 0
+    for j in range(0, 256, 64):
+        sc, m = get_scale_min_k4(is_, scales)
+        d1, m1 = d * sc, dmin * m
+        sc, m = get_scale_min_k4(is_ + 1, scales)
+        d2, m2 = d * sc, dmin * m
+        qq = q[(j // 64) * 32:(j // 64) * 32 + 32]
+        y[j:j + 32] = d1 * (qq & 0xF) - m1
+        y[j + 32:j + 64] = d2 * (qq >> 4) - m2
+        is_ += 2
+    return y
+
+
+def random_kblocks(rng, qtype: int, n: int) -> np.ndarray:
+    raw = rng.integers(0, 256, (n, oracle.BLOCK_BYTES[qtype]), dtype=np.uint8)
+    scale = rng.uniform(0.001, 0.02, (n, 2)).astype(np.float16)
+    if qtype == oracle.Q6_K:
+        raw[:, 208:210] = scale[:, :1].view(np.uint8).reshape(n, 2)
+    else:
+        raw[:, 0:4] = scale.view(np.uint8).reshape(n, 4)
+    return raw
+
+
+@pytest.mark.parametrize("qtype,ref", [(oracle.Q6_K, ggml_q6_k_row), (oracle.Q4_K, ggml_q4_k_row)])
+def test_kquant_dequant_matches_ggml_loops(qtype, ref):
+    rng = np.random.default_rng(90 + qtype)
+    blocks = random_kblocks(rng, qtype, 12)
+    flat = blocks.reshape(-1)
+    for b in range(blocks.shape[0]):
+        want = ref(blocks[b])
+        got = np.array([oracle.dequant(qtype, flat, 256 * b + e) for e in range(256)])
+        # every weight is an exact product in fp32 (Q4_K: one rounding of the difference)
+        np.testing.assert_allclose(got, want, rtol=2 ** -23, atol=0)
+
+
+def test_kquant_closed_forms():
+    z6 = np.zeros(210, np.uint8)
+    z6[208:210] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+    z6[192:208] = 1
+    assert [oracle.dequant(oracle.Q6_K, z6, e) for e in range(256)] == [-32.0] * 256
+    for e in range(256):  # a single ql nibble lifts one element by 1
+        b = z6.copy()
+        half, pos = divmod(e, 128)
+        sub, l = divmod(pos, 32)
+        b[64 * half + l + (32 if sub & 1 else 0)] |= 0x1 if sub < 2 else 0x10
+        vals = [oracle.dequant(oracle.Q6_K, b, k) for k in range(256)]
+        assert vals == [-31.0 if k == e else -32.0 for k in range(256)], e
+    z4 = np.zeros(144, np.uint8)
+    z4[0:2] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+    z4[4:8] = 1  # sub-blocks 0-3: scale 1, min 0; 4-7: scale (b[8+j] & 15) = 0
+    vals = [oracle.dequant(oracle.Q4_K, z4, e) for e in range(256)]
+    assert vals == [0.0] * 256
+    z4[16:144] = 0x21  # low nibble 1, high nibble 2
+    vals = [oracle.dequant(oracle.Q4_K, z4, e) for e in range(256)]
+    assert vals[:128] == [1.0] * 32 + [2.0] * 32 + [1.0] * 32 + [2.0] * 32 and vals[128:] == [0.0] * 128
+
+
+@pytest.mark.parametrize("qtype", [oracle.Q6_K, oracle.Q4_K])
+def test_kquant_matmul_against_float64(qtype):
+    rng = np.random.default_rng(95 + qtype)
+    rows, cols = 24, 1024
+    w = random_kblocks(rng, qtype, rows * cols // 256).reshape(-1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    ref = ggml_q6_k_row if qtype == oracle.Q6_K else ggml_q4_k_row
+    w64 = np.concatenate([ref(b) for b in w.reshape(-1, oracle.BLOCK_BYTES[qtype])]).reshape(rows, cols)
+    y64 = w64 @ x.astype(np.float64)
+    got = oracle.matmul_q(qtype, w, x, rows, cols).astype(np.float64)
+    bound = (cols + 2) * 2.0 ** -24 * (np.abs(w64) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(got - y64) <= bound)
+    with pytest.raises(ValueError):
+        oracle.matmul_q(qtype, w, x, rows, 896)

@@ -110,6 +110,19 @@ struct QkvArgs {
 };
 constexpr int kQkvWaves = 4;         // output rows per workgroup (one wave each)
 
+// y = W x (+ bias) for K-quant weights: rows of cols / 256 super-blocks, Q4_K
+// (type 12, 144 bytes) or Q6_K (type 14, 210 bytes).  bias may equal y (the
+// residual form y += W x).
+struct KqArgs {
+    const uint8_t* w;
+    const float* x;          // [cols], 16-byte aligned
+    const float* bias;
+    float* y;
+    int rows;
+    int cols;
+    int type;
+};
+
 struct PosArgs {
     int* pos;
     int value;

@@ -1254,6 +1254,73 @@ extern "C" __global__ __launch_bounds__(256) void tmac_copy(CopyArgs a) {
     if (i < a.n) a.dst[i] = a.add ? a.dst[i] + a.src[i] : a.src[i];
 }
 
+// K-quant GEMV (matmul_q4_k / matmul_q6_k, metal_backend.hpp:340-350;
+// dequantisation tmac_gguf.cpp:330-397): one wave per output row, lane l takes
+// elements 4l .. 4l+3 of each 256-weight super-block, which share one sub-block
+// scale (and, for Q4_K, one min).  Super-blocks start at even offsets, so their
+// bytes are read as 16-bit words.  Each dequantised weight is the reference's
+// expression (Q6_K: d * scale * q, exact; Q4_K: d * sc * q - dmin * m, exact
+// products and one rounding); the row sum is one FMA per element and a wave
+// reduction.
+extern "C" __global__ __launch_bounds__(kQkvWaves * 64) void tmac_matmul_kq(KqArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kQkvWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (r >= a.rows) return;
+    const int nsb = a.cols >> 8;
+    const bool q6 = a.type == 14;
+    const int bytes = q6 ? 210 : 144;
+    const uint8_t* wrow = a.w + (size_t)r * nsb * bytes;
+    float acc = 0.f;
+    for (int sb = 0; sb < nsb; ++sb) {
+        const uint8_t* blk = wrow + (size_t)sb * bytes;
+        const float4 xv = *reinterpret_cast<const float4*>(a.x + 256 * sb + 4 * lane);
+        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+        float w[4];
+        if (q6) {
+            const int half = lane >> 5, sub = (lane >> 3) & 3, l0 = 4 * (lane & 7);
+            const float d = half_bits_to_float(ld16(blk + 208));
+            const float dsc = d * (float)(int8_t)blk[192 + half * 8 + (l0 >> 4) + 2 * sub];
+            const uint8_t* ql = blk + half * 64 + l0 + ((sub & 1) ? 32 : 0);
+            const uint8_t* qh = blk + 128 + half * 32 + l0;
+            const unsigned qlw = ld16(ql) | (ld16(ql + 2) << 16);
+            const unsigned qhw = ld16(qh) | (ld16(qh + 2) << 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned lb = (qlw >> (8 * i)) & 0xFF;
+                const unsigned lo = sub < 2 ? (lb & 0xF) : (lb >> 4);
+                const unsigned hi = ((qhw >> (8 * i)) >> (2 * sub)) & 0x3;
+                w[i] = dsc * (float)((int)((hi << 4) | lo) - 32);
+            }
+        } else {
+            const int sbk = lane >> 3, q_pos = 4 * (lane & 7);
+            const float d = half_bits_to_float(ld16(blk));
+            const float dmin = half_bits_to_float(ld16(blk + 2));
+            const uint8_t* sc6 = blk + 4;
+            unsigned sc, m;
+            if (sbk < 4) {
+                sc = sc6[sbk] & 63;
+                m = sc6[sbk + 4] & 63;
+            } else {
+                sc = (sc6[sbk + 4] & 0xF) | ((sc6[sbk - 4] >> 6) << 4);
+                m = (sc6[sbk + 4] >> 4) | ((sc6[sbk] >> 6) << 4);
+            }
+            const uint8_t* qs = blk + 16 + (sbk >> 1) * 32 + q_pos;
+            const unsigned qw = ld16(qs) | (ld16(qs + 2) << 16);
+            const float dsc = d * (float)sc, dm = dmin * (float)m;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned b = (qw >> (8 * i)) & 0xFF;
+                const unsigned q4 = (sbk & 1) ? (b >> 4) : (b & 0xF);
+                w[i] = dsc * (float)q4 - dm;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(w[i], xs[i], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) a.y[r] = a.bias ? acc + a.bias[r] : acc;
+}
+
 // Fills a 16-bit cache from fp32 values, rounding to nearest even.
 extern "C" __global__ __launch_bounds__(256) void tmac_cvt16(CvtArgs a) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

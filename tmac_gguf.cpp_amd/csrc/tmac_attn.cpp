@@ -37,6 +37,7 @@ using tmac::kPrefillStageTiles;
 using tmac::kPrefillTileElems;
 using tmac::kPrefillWaves;
 using tmac::PosArgs;
+using tmac::KqArgs;
 using tmac::QkvArgs;
 using tmac::kQkvWaves;
 using tmac::RopeArgs;
@@ -81,7 +82,8 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head16[2][3];    // 16-bit caches: head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
-    hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr;
+    hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
+                  k_kq = nullptr;
     float* ws = nullptr;
     size_t ws_floats = 0;
     int* err = nullptr;
@@ -448,7 +450,8 @@ int tmac_init(tmac_context** out, int device) {
         (e = hipModuleGetFunction(&ctx->k_copy, ctx->module, "tmac_copy")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->k_pos, ctx->module, "tmac_pos_update")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->k_qkv, ctx->module, "tmac_qkv")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_cvt16, ctx->module, "tmac_cvt16")) != hipSuccess)
+        (e = hipModuleGetFunction(&ctx->k_cvt16, ctx->module, "tmac_cvt16")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->k_kq, ctx->module, "tmac_matmul_kq")) != hipSuccess)
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
@@ -796,10 +799,22 @@ static int matmul_common(tmac_context* ctx, hipStream_t stream, int qtype, int r
                          const float* x, float* y, bool accumulate) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
-    if (qtype != TMAC_Q5_0 && qtype != TMAC_Q8_0)
-        return fail(ctx, TMAC_ERR_UNSUPPORTED, "matmul: weight type must be TMAC_Q5_0 or TMAC_Q8_0");
+    if (qtype != TMAC_Q5_0 && qtype != TMAC_Q8_0 && qtype != TMAC_Q4_K && qtype != TMAC_Q6_K)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "matmul: weight type must be TMAC_Q5_0, _Q8_0, _Q4_K or _Q6_K");
     if (x && y && (const void*)x == (const void*)y)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "matmul: x and y must not overlap");
+    if (qtype == TMAC_Q4_K || qtype == TMAC_Q6_K) {
+        if (rows < 0 || cols <= 0 || cols % 256 || rows > INT_MAX - kQkvWaves)
+            return fail(ctx, TMAC_ERR_INVALID_ARG, "matmul: K-quant rows >= 0 and cols a positive multiple of 256");
+        if (!w || !x || !y) return fail(ctx, TMAC_ERR_NULL_POINTER, "matmul: null buffer");
+        if (!aligned16(x) || (uintptr_t)w % 2 || (uintptr_t)y % 4)
+            return fail(ctx, TMAC_ERR_MISALIGNED, "matmul: x 16-byte, weights 2-byte, y 4-byte aligned");
+        if (rows == 0) return TMAC_OK;
+        if ((rc = set_device(ctx))) return rc;
+        KqArgs a{(const uint8_t*)w, x, accumulate ? y : nullptr, y, rows, cols, qtype};
+        return launch(ctx, ctx->k_kq, (unsigned)((rows + kQkvWaves - 1) / kQkvWaves), 1, kQkvWaves * 64, stream,
+                      &a);
+    }
     return qkv_common(ctx, stream, nullptr, nullptr, w, x, nullptr, nullptr, accumulate ? y : nullptr, nullptr,
                       nullptr, y, 0, 0, rows, cols, qtype == TMAC_Q8_0);
 }
@@ -812,6 +827,16 @@ int tmac_matmul_q8_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, 
 int tmac_matmul_q5_0(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
                      float* y) {
     return matmul_common(ctx, (hipStream_t)stream, TMAC_Q5_0, rows, cols, w, x, y, false);
+}
+
+int tmac_matmul_q4_k(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y) {
+    return matmul_common(ctx, (hipStream_t)stream, TMAC_Q4_K, rows, cols, w, x, y, false);
+}
+
+int tmac_matmul_q6_k(tmac_context* ctx, tmac_stream stream, int rows, int cols, const void* w, const float* x,
+                     float* y) {
+    return matmul_common(ctx, (hipStream_t)stream, TMAC_Q6_K, rows, cols, w, x, y, false);
 }
 
 int tmac_matmul_add(tmac_context* ctx, tmac_stream stream, int qtype, int rows, int cols, const void* w,

@@ -34,6 +34,8 @@ TMAC_ERR_HIP_BASE = 1000
 
 TMAC_Q5_0 = 6
 TMAC_Q8_0 = 8
+TMAC_Q4_K = 12
+TMAC_Q6_K = 14
 TMAC_KV_F32 = 0
 TMAC_KV_BF16 = 1
 TMAC_KV_F16 = 2
@@ -76,6 +78,8 @@ SIGNATURES = {
     "tmac_matmul_q8_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "tmac_matmul_q5_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "tmac_matmul_add": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "tmac_matmul_q4_k": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "tmac_matmul_q6_k": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "tmac_layer_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f]),
     "tmac_layer_attention_devpos": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _f]),
     "tmac_pos_update": (_i, [_vp, _vp, _vp, _i, _i]),
@@ -321,6 +325,10 @@ class Context:
             rc = self.lib.tmac_matmul_add(self.handle, stream, qtype, rows, cols, _p(w), _p(x), _p(y))
         elif qtype == TMAC_Q8_0:
             rc = self.lib.tmac_matmul_q8_0(self.handle, stream, rows, cols, _p(w), _p(x), _p(y))
+        elif qtype == TMAC_Q4_K:
+            rc = self.lib.tmac_matmul_q4_k(self.handle, stream, rows, cols, _p(w), _p(x), _p(y))
+        elif qtype == TMAC_Q6_K:
+            rc = self.lib.tmac_matmul_q6_k(self.handle, stream, rows, cols, _p(w), _p(x), _p(y))
         else:
             rc = self.lib.tmac_matmul_q5_0(self.handle, stream, rows, cols, _p(w), _p(x), _p(y))
         if check:
