@@ -54,6 +54,8 @@ enum tmac_status {
     TMAC_ERR_NOT_INITIALIZED = 6,
     TMAC_ERR_CAPTURE = 7,         /* needs an allocation while the stream is being captured */
     TMAC_ERR_DEVICE_FAULT = 8,    /* a kernel reported a bad device-side position */
+    TMAC_ERR_NOT_FOUND = 9,       /* no tensor of that name in a loaded weight file */
+    TMAC_ERR_IO = 10,             /* weight file missing, truncated or not in TMAC format */
     TMAC_ERR_HIP_BASE = 1000      /* TMAC_ERR_HIP_BASE + hipError_t */
 };
 
@@ -182,6 +184,32 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
                                  const float* k_pool, const float* v_pool, const int64_t* offsets,
                                  const int32_t* lengths, float* out, int n_seq, int n_head,
                                  int n_kv_head, int head_dim, int max_len, int64_t total_rows);
+
+/* ---- TMAC weight file: load_tmac (tmac_gguf.cpp:1372-1425) ----
+ * The file scripts/extract_tmac.py writes (its :1-24, 261-272):
+ *   "TMAC", u64 n_tensors, then per tensor u64 name_len, name bytes, u64 rows,
+ *   u64 cols, u32 type (tmac_weight_type), u64 n_bytes, n_bytes of data
+ * (little endian).  rows / cols are as stored: rows = outputs (ne[1]), cols =
+ * inputs (ne[0]).  With a context the tensors are copied to one device
+ * allocation (each at a 256-byte aligned offset); with ctx == NULL they stay in
+ * host memory (inspection without a GPU).  Names of 128 bytes or more are cut
+ * to their first 127, as the reference does; lookups return the first tensor
+ * of a name, as get_tensor_info does.  Unlike the reference, the magic is
+ * checked and there is no 512 MiB cap (TMAC_ERR_IO on a short or foreign file). */
+typedef struct tmac_model tmac_model;
+typedef struct {
+    const char* name;  /* owned by the model */
+    uint64_t rows, cols;
+    uint32_t type;
+    uint64_t n_bytes;
+    void* data;        /* device pointer, or host pointer for a model loaded without a context */
+} tmac_tensor_info;
+int tmac_model_load(tmac_context* ctx, const char* path, tmac_model** model);
+int tmac_model_count(const tmac_model* model);  /* number of tensors, or a negative status */
+int tmac_model_tensor(const tmac_model* model, int index, tmac_tensor_info* info);
+int tmac_model_find(const tmac_model* model, const char* name, tmac_tensor_info* info);  /* TMAC_ERR_NOT_FOUND */
+/* Frees the model's memory; ctx must be the context it was loaded with (NULL for a host model). */
+int tmac_model_free(tmac_context* ctx, tmac_model* model);
 
 /* ---- 16-bit KV caches (extension; the reduced-precision cache motivated at
  *      LLAMACPP_METAL_STUDY.md:50-54) ----

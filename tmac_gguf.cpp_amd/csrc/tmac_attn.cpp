@@ -18,7 +18,9 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <string>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -66,6 +68,21 @@ struct RopeTable {
 
 struct tmac_graph {
     hipGraphExec_t exec = nullptr;
+};
+
+struct tmac_model {
+    struct Entry {
+        std::string name;
+        uint64_t rows = 0, cols = 0, n_bytes = 0;
+        uint32_t type = 0;
+        size_t offset = 0;  // into blob, 256-byte aligned
+    };
+    std::vector<Entry> tensors;
+    std::unordered_map<std::string, size_t> index;  // name -> first tensor of that name
+    uint8_t* blob = nullptr;                        // device allocation, or 256-byte aligned inside host
+    std::unique_ptr<uint8_t[]> host;
+    size_t bytes = 0;
+    bool on_device = false;
 };
 
 struct tmac_context {
@@ -351,6 +368,8 @@ const char* tmac_status_string(int status) {
         case TMAC_ERR_NOT_INITIALIZED: return "context not initialized";
         case TMAC_ERR_CAPTURE: return "not allowed while the stream is capturing";
         case TMAC_ERR_DEVICE_FAULT: return "device reported an out-of-range position";
+        case TMAC_ERR_NOT_FOUND: return "no tensor of that name";
+        case TMAC_ERR_IO: return "weight file missing, truncated or not a TMAC file";
         default: break;
     }
     if (status >= TMAC_ERR_HIP_BASE) return hipGetErrorString((hipError_t)(status - TMAC_ERR_HIP_BASE));
@@ -1085,6 +1104,128 @@ int tmac_device_info(tmac_context* ctx, char* buf, size_t buf_len, int* n_cu) {
                       p.name, p.gcnArchName, p.multiProcessorCount, p.clockRate, p.memoryClockRate,
                       p.memoryBusWidth, (size_t)p.totalGlobalMem, p.l2CacheSize);
     }
+    return TMAC_OK;
+}
+
+// ---- TMAC weight file (load_tmac, tmac_gguf.cpp:1372-1425) ----
+
+int tmac_model_load(tmac_context* ctx, const char* path, tmac_model** model) {
+    if (ctx) {
+        int rc = check_ctx(ctx);
+        if (rc) return rc;
+    }
+    if (!path || !model) return fail(ctx, TMAC_ERR_NULL_POINTER, "model_load: null argument");
+    *model = nullptr;
+    std::unique_ptr<FILE, int (*)(FILE*)> f(std::fopen(path, "rb"), &std::fclose);
+    if (!f) return fail(ctx, TMAC_ERR_IO, std::string("model_load: cannot open ") + path);
+    if (fseeko(f.get(), 0, SEEK_END) != 0) return fail(ctx, TMAC_ERR_IO, "model_load: cannot seek");
+    const uint64_t file_bytes = (uint64_t)ftello(f.get());
+    fseeko(f.get(), 0, SEEK_SET);
+    auto rd = [&](void* p, size_t n) { return std::fread(p, 1, n, f.get()) == n; };
+    char magic[4];
+    uint64_t n_tensors = 0;
+    if (!rd(magic, 4) || std::memcmp(magic, "TMAC", 4) != 0 || !rd(&n_tensors, 8))
+        return fail(ctx, TMAC_ERR_IO, "model_load: not a TMAC file");
+    if (n_tensors > (file_bytes - 12) / 36)  // each entry holds at least 36 bytes of header
+        return fail(ctx, TMAC_ERR_IO, "model_load: tensor count larger than the file");
+    std::unique_ptr<tmac_model> m(new tmac_model());
+    std::vector<uint64_t> file_off(n_tensors);
+    size_t total = 0;
+    for (uint64_t i = 0; i < n_tensors; i++) {
+        tmac_model::Entry e;
+        uint64_t name_len = 0;
+        if (!rd(&name_len, 8) || name_len > file_bytes)
+            return fail(ctx, TMAC_ERR_IO, "model_load: truncated at tensor " + std::to_string(i));
+        const uint64_t keep = name_len < 128 ? name_len : 127;  // the reference keeps 127 characters
+        e.name.resize(keep);
+        if (!rd(&e.name[0], keep) || (name_len > keep && fseeko(f.get(), (off_t)(name_len - keep), SEEK_CUR) != 0))
+            return fail(ctx, TMAC_ERR_IO, "model_load: truncated name at tensor " + std::to_string(i));
+        e.name.resize(std::strlen(e.name.c_str()));  // a NUL inside the name ends it, as a C string read does
+        if (!rd(&e.rows, 8) || !rd(&e.cols, 8) || !rd(&e.type, 4) || !rd(&e.n_bytes, 8))
+            return fail(ctx, TMAC_ERR_IO, "model_load: truncated header at tensor " + std::to_string(i));
+        const uint64_t at = (uint64_t)ftello(f.get());
+        if (e.n_bytes > file_bytes - at)
+            return fail(ctx, TMAC_ERR_IO, "model_load: data of tensor " + std::to_string(i) + " runs past the end");
+        file_off[i] = at;
+        fseeko(f.get(), (off_t)e.n_bytes, SEEK_CUR);
+        total = (total + 255) & ~size_t(255);
+        e.offset = total;
+        total += e.n_bytes;
+        m->index.emplace(e.name, m->tensors.size());  // keeps the first tensor of a name
+        m->tensors.push_back(std::move(e));
+    }
+    m->bytes = total;
+    std::vector<uint8_t> staging;
+    if (ctx) {
+        int rc = set_device(ctx);
+        if (rc) return rc;
+        if (total) HIP_TRY(ctx, hipMalloc(&m->blob, total));
+        m->on_device = true;
+    } else {
+        m->host.reset(new uint8_t[total + 256]);  // aligned below, as device allocations are
+        m->blob = reinterpret_cast<uint8_t*>((reinterpret_cast<uintptr_t>(m->host.get()) + 255) & ~uintptr_t(255));
+    }
+    for (size_t i = 0; i < m->tensors.size(); i++) {
+        const tmac_model::Entry& e = m->tensors[i];
+        uint8_t* dst = m->blob + e.offset;
+        if (m->on_device) {
+            staging.resize(e.n_bytes);
+            dst = staging.data();
+        }
+        if (fseeko(f.get(), (off_t)file_off[i], SEEK_SET) != 0 || !rd(dst, e.n_bytes)) {
+            if (m->on_device) (void)hipFree(m->blob);
+            return fail(ctx, TMAC_ERR_IO, "model_load: cannot read tensor " + e.name);
+        }
+        if (m->on_device && e.n_bytes) {
+            const hipError_t err = hipMemcpy(m->blob + e.offset, staging.data(), e.n_bytes, hipMemcpyHostToDevice);
+            if (err != hipSuccess) {
+                (void)hipFree(m->blob);
+                return hip_fail(ctx, err, "model_load: hipMemcpy");
+            }
+        }
+    }
+    *model = m.release();
+    return TMAC_OK;
+}
+
+int tmac_model_count(const tmac_model* model) {
+    return model ? (int)model->tensors.size() : -TMAC_ERR_NULL_POINTER;
+}
+
+static void fill_info(const tmac_model* m, size_t i, tmac_tensor_info* info) {
+    const tmac_model::Entry& e = m->tensors[i];
+    info->name = e.name.c_str();
+    info->rows = e.rows;
+    info->cols = e.cols;
+    info->type = e.type;
+    info->n_bytes = e.n_bytes;
+    info->data = m->blob + e.offset;
+}
+
+int tmac_model_tensor(const tmac_model* model, int index, tmac_tensor_info* info) {
+    if (!model || !info) return TMAC_ERR_NULL_POINTER;
+    if (index < 0 || (size_t)index >= model->tensors.size()) return TMAC_ERR_INVALID_ARG;
+    fill_info(model, (size_t)index, info);
+    return TMAC_OK;
+}
+
+int tmac_model_find(const tmac_model* model, const char* name, tmac_tensor_info* info) {
+    if (!model || !name || !info) return TMAC_ERR_NULL_POINTER;
+    auto it = model->index.find(name);
+    if (it == model->index.end()) return TMAC_ERR_NOT_FOUND;
+    fill_info(model, it->second, info);
+    return TMAC_OK;
+}
+
+int tmac_model_free(tmac_context* ctx, tmac_model* model) {
+    if (!model) return TMAC_OK;
+    if (model->on_device) {
+        if (!ctx) return TMAC_ERR_INVALID_ARG;  // a device model needs its context
+        int rc = set_device(ctx);
+        if (rc) return rc;
+        if (model->blob) (void)hipFree(model->blob);
+    }
+    delete model;
     return TMAC_OK;
 }
 

@@ -30,6 +30,8 @@ TMAC_ERR_CAPACITY = 5
 TMAC_ERR_NOT_INITIALIZED = 6
 TMAC_ERR_CAPTURE = 7
 TMAC_ERR_DEVICE_FAULT = 8
+TMAC_ERR_NOT_FOUND = 9
+TMAC_ERR_IO = 10
 TMAC_ERR_HIP_BASE = 1000
 
 TMAC_Q5_0 = 6
@@ -109,7 +111,60 @@ SIGNATURES = {
     "tmac_event_record": (_i, [_vp, _vp, _vp]),
     "tmac_event_elapsed_ms": (_i, [_vp, _vp, _vp, ctypes.POINTER(_f)]),
     "tmac_device_info": (_i, [_vp, ctypes.c_char_p, _sz, ctypes.POINTER(_i)]),
+    "tmac_model_load": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "tmac_model_count": (_i, [_vp]),
+    "tmac_model_tensor": (_i, [_vp, _i, _vp]),
+    "tmac_model_find": (_i, [_vp, ctypes.c_char_p, _vp]),
+    "tmac_model_free": (_i, [_vp, _vp]),
 }
+
+
+class TensorInfo(ctypes.Structure):
+    """tmac_tensor_info."""
+    _fields_ = [("name", ctypes.c_char_p), ("rows", ctypes.c_uint64), ("cols", ctypes.c_uint64),
+                ("type", ctypes.c_uint32), ("n_bytes", ctypes.c_uint64), ("data", ctypes.c_void_p)]
+
+
+class Model:
+    """A loaded TMAC weight file (tmac_model_load).  `ctx=None` keeps the
+    tensors in host memory; with a Context they live on the device."""
+
+    def __init__(self, path: str, ctx: Optional["Context"] = None):
+        self.lib = load_library()
+        self.ctx = ctx
+        h = _vp()
+        rc = self.lib.tmac_model_load(ctx.handle if ctx else None, os.fsencode(path), ctypes.byref(h))
+        if rc != TMAC_OK:
+            detail = self.lib.tmac_last_error(ctx.handle).decode() if ctx else path
+            raise TmacError(rc, "model_load", detail)
+        self.handle = h.value
+
+    def __len__(self) -> int:
+        return self.lib.tmac_model_count(self.handle)
+
+    def _info(self, rc: int, info: TensorInfo, what: str) -> dict:
+        if rc != TMAC_OK:
+            raise TmacError(rc, what)
+        return {"name": info.name.decode(), "rows": info.rows, "cols": info.cols, "type": info.type,
+                "n_bytes": info.n_bytes, "data": info.data}
+
+    def tensor(self, index: int) -> dict:
+        info = TensorInfo()
+        return self._info(self.lib.tmac_model_tensor(self.handle, index, ctypes.byref(info)), info, "model_tensor")
+
+    def find(self, name: str) -> Optional[dict]:
+        info = TensorInfo()
+        rc = self.lib.tmac_model_find(self.handle, name.encode(), ctypes.byref(info))
+        if rc == TMAC_ERR_NOT_FOUND:
+            return None
+        return self._info(rc, info, "model_find")
+
+    def free(self) -> None:
+        if self.handle:
+            rc = self.lib.tmac_model_free(self.ctx.handle if self.ctx else None, self.handle)
+            if rc != TMAC_OK:
+                raise TmacError(rc, "model_free")
+            self.handle = None
 
 _lib: Optional[ctypes.CDLL] = None
 
