@@ -108,28 +108,70 @@ def bench_c3(ctx, stream, steps, warmup, n_seq=256, n_pos=4096):
     return res, (q, k, v, out, n_seq, n_pos)
 
 
-def bench_kv16(ctx, stream, steps, warmup, dtype_name, n_seq=256, n_pos=4096):
-    """Config 3's workload on a 16-bit cache (tmac_attention_decode_batched_kv):
-    the same rows, half the bytes.  K/V are drawn as in config 3 and converted
-    on the device (tmac_kv_convert)."""
+KV_TYPES = {"f32": 0, "bf16": 1, "f16": 2, "q8": 3}  # tmac_kv_dtype
+ROW_BYTES_BY_TYPE = {"f32": KVD * 4, "bf16": KVD * 2, "f16": KVD * 2, "q8": NKV * 68}
+
+
+def _narrow_cache(ctx, rng, dtype_name, rows):
+    """`rows` cache rows of N(0,1) values in the named element type, converted
+    on the device (tmac_kv_convert) from fp32 drawn as in config 3."""
     import tmac_attn
-    dt = {"bf16": tmac_attn.TMAC_KV_BF16, "f16": tmac_attn.TMAC_KV_F16}[dtype_name]
+    dt = KV_TYPES[dtype_name]
+    if dt == 0:
+        return ctx.upload(rng.standard_normal((rows, KVD), dtype=np.float32))
+    dst = ctx.empty(rows * ROW_BYTES_BY_TYPE[dtype_name], np.uint8)
+    chunk = 1 << 20  # rows per conversion (bounded staging buffer)
+    for r0 in range(0, rows, chunk):
+        n = min(chunk, rows - r0)
+        tmp = ctx.upload(rng.standard_normal((n, KVD), dtype=np.float32))
+        ctx.kv_convert(dt, tmp, dst.at(r0 * ROW_BYTES_BY_TYPE[dtype_name]), n * KVD)
+        ctx.synchronize()
+        tmp.free()
+    return dst
+
+
+def bench_kvn(ctx, stream, steps, warmup, dtype_name, n_seq=256, n_pos=4096):
+    """Config 3's workload on a narrow cache (tmac_attention_decode_batched_kv):
+    the same rows, bf16/fp16 half the bytes, Q8_0 0.27x."""
+    dt = KV_TYPES[dtype_name]
     rng = np.random.default_rng(3)
     q = rng.standard_normal((n_seq, NH * HD), dtype=np.float32)
     dq, dout = ctx.upload(q), ctx.empty((n_seq, NH * HD))
-    dk16, dv16 = ctx.empty(n_seq * n_pos * KVD, np.uint16), ctx.empty(n_seq * n_pos * KVD, np.uint16)
-    for d16 in (dk16, dv16):
-        tmp = ctx.upload(rng.standard_normal((n_seq * n_pos, KVD), dtype=np.float32))
-        ctx.kv_convert(dt, tmp, d16, n_seq * n_pos * KVD)
-        ctx.synchronize()
-        tmp.free()
+    dk, dv = _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos), _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos)
 
     def launch():
-        ctx.decode_batched(dq, dk16, dv16, dout, n_seq, NH, NKV, HD, n_pos, n_pos, stream=stream, kv_dtype=dt)
+        ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, stream=stream, kv_dtype=dt)
 
     per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
-    nbytes = n_seq * (n_pos * KVD * 2 * 2 + 2 * NH * HD * 4)  # K + V 16-bit, q + out fp32
-    for d in (dq, dout, dk16, dv16):
+    nbytes = n_seq * (n_pos * ROW_BYTES_BY_TYPE[dtype_name] * 2 + 2 * NH * HD * 4)  # K + V, q + out fp32
+    for d in (dq, dout, dk, dv):
+        d.free()
+    return {"bytes": nbytes, "mean_us": mean_ms * 1e3, "median_us": float(np.median(per)) * 1e3,
+            "gbs": nbytes / (mean_ms * 1e-3) / 1e9, "pct_of_peak": nbytes / (mean_ms * 1e-3) / 1e9 / 80.0,
+            "rows_per_s": n_seq * n_pos / (mean_ms * 1e-3)}
+
+
+def bench_paged(ctx, stream, steps, warmup, dtype_name, n_seq=256, n_pos=4096):
+    """Config 3's workload on a paged cache (tmac_attention_decode_paged):
+    16-row pages scattered over the pool in a random order, as a serving
+    allocator leaves them.  Bytes also count the block-table entries read."""
+    dt = KV_TYPES[dtype_name]
+    page_rows = 16
+    rng = np.random.default_rng(3)
+    n_pages = n_seq * n_pos // page_rows
+    table = rng.permutation(n_pages).astype(np.int32).reshape(n_seq, n_pos // page_rows)
+    lens = np.full(n_seq, n_pos, np.int32)
+    q = rng.standard_normal((n_seq, NH * HD), dtype=np.float32)
+    dq, dout, dtab, dlen = ctx.upload(q), ctx.empty((n_seq, NH * HD)), ctx.upload(table), ctx.upload(lens)
+    dk, dv = _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos), _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos)
+
+    def launch():
+        ctx.decode_paged(dq, dk, dv, n_pages, dtab, table.shape[1], dlen, dout, n_seq, NH, NKV, HD, n_pos,
+                         stream=stream, kv_dtype=dt)
+
+    per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
+    nbytes = n_seq * (n_pos * ROW_BYTES_BY_TYPE[dtype_name] * 2 + 2 * NH * HD * 4 + 4) + table.nbytes
+    for d in (dq, dout, dtab, dlen, dk, dv):
         d.free()
     return {"bytes": nbytes, "mean_us": mean_ms * 1e3, "median_us": float(np.median(per)) * 1e3,
             "gbs": nbytes / (mean_ms * 1e-3) / 1e9, "pct_of_peak": nbytes / (mean_ms * 1e-3) / 1e9 / 80.0,
@@ -426,8 +468,9 @@ def main():
     ap.add_argument("--target-groups", type=int, default=None, help="override TMAC_OPT_TARGET_GROUPS (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
-    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv,kv16",
-                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv,kv16")
+    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv,kv,paged",
+                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv,kv (bf16, "
+                         "fp16, Q8_0 caches), kv16 (bf16, fp16 only), paged")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -474,11 +517,17 @@ def main():
     if "c4" in sections:
         extra["c4"] = bench_c4(ctx, stream, max(10, args.steps // 2), args.warmup)
         log(f"[bench] C4 {extra['c4']['gbs']:.1f} GB/s")
-    for tn in ("bf16", "f16"):
-        if "kv16" in sections or f"kv_{tn}" in sections:
-            extra[f"c3_{tn}"] = bench_kv16(ctx, stream, args.steps, args.warmup, tn)
+    for tn in ("bf16", "f16", "q8"):
+        if "kv" in sections or ("kv16" in sections and tn != "q8") or f"kv_{tn}" in sections:
+            extra[f"c3_{tn}"] = bench_kvn(ctx, stream, args.steps, args.warmup, tn)
             r = extra[f"c3_{tn}"]
             log(f"[bench] C3 {tn} cache: {r['mean_us']:.1f} us/launch, {r['gbs']:.1f} GB/s "
+                f"({r['pct_of_peak']:.1f}% of peak), {r['rows_per_s'] / 1e9:.2f} G rows/s")
+    for tn in ("f32", "q8"):
+        if "paged" in sections or f"paged_{tn}" in sections:
+            extra[f"c3_paged_{tn}"] = bench_paged(ctx, stream, args.steps, args.warmup, tn)
+            r = extra[f"c3_paged_{tn}"]
+            log(f"[bench] C3 paged {tn} cache: {r['mean_us']:.1f} us/launch, {r['gbs']:.1f} GB/s "
                 f"({r['pct_of_peak']:.1f}% of peak), {r['rows_per_s'] / 1e9:.2f} G rows/s")
     if "qkv" in sections:
         extra["qkv"] = bench_qkv(ctx, stream, args.steps, args.warmup)

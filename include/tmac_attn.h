@@ -211,16 +211,25 @@ int tmac_model_find(const tmac_model* model, const char* name, tmac_tensor_info*
 /* Frees the model's memory; ctx must be the context it was loaded with (NULL for a host model). */
 int tmac_model_free(tmac_context* ctx, tmac_model* model);
 
-/* ---- 16-bit KV caches (extension; the reduced-precision cache motivated at
+/* ---- reduced-precision KV caches (extension; the quantized cache motivated at
  *      LLAMACPP_METAL_STUDY.md:50-54) ----
- * The same cache layout with bf16 or fp16 elements instead of fp32: half the
- * bytes on the HBM-bound path.  Rows are read and widened exactly to fp32, so
- * each call equals the fp32 path run on the widened cache (the tolerance
- * contract: |out - oracle(widen(cache))| <= 2e-5 + 1e-4 |ref|).  The layer
- * step rounds the rotated k and v_new to the cache type (nearest even) before
- * it stores them and attends the stored values.  These calls use the default
- * 8-wave group and head kernels whatever TMAC_OPT_GROUP_WAVES / _HEAD_WAVES say. */
-enum tmac_kv_dtype { TMAC_KV_F32 = 0, TMAC_KV_BF16 = 1, TMAC_KV_F16 = 2 };
+ * The same cache layout with narrower elements: bf16 or fp16 (half the bytes
+ * on the HBM-bound path), or Q8_0 (0.27x).  A Q8_0 cache stores each
+ * (row, kv head) as a 68-byte head row: int8 q[64], then the fp16 scales d0
+ * (dims 0..31) and d1 (dims 32..63), i.e. the two GGML Q8_0 blocks of those
+ * 64 values (dequant_q8_0, tmac_gguf.cpp:240-250: value = q * d) with the
+ * scales moved behind the values; a cache row is n_kv_head * 68 bytes.
+ * Rows are read and widened exactly to fp32, so each call equals the fp32
+ * path run on the widened cache (the tolerance contract:
+ * |out - oracle(widen(cache))| <= 2e-5 + 1e-4 |ref|).  The layer step turns
+ * the rotated k and v_new into the cache type before it stores and attends
+ * them: bf16/fp16 round to nearest even; Q8_0 quantizes each 32-value block
+ * as the reference's quantize_q8_0_block does (scripts/extract_tmac.py:159-173:
+ * d = max|x| / 127, or 1 when max|x| < 1e-10; q = x / d rounded half to even;
+ * d stored with float_to_fp16, :53-74, which truncates the mantissa and
+ * flushes fp16-subnormal values to 0).  These calls use the default 8-wave
+ * group and head kernels whatever TMAC_OPT_GROUP_WAVES / _HEAD_WAVES say. */
+enum tmac_kv_dtype { TMAC_KV_F32 = 0, TMAC_KV_BF16 = 1, TMAC_KV_F16 = 2, TMAC_KV_Q8_0 = 3 };
 int tmac_attention_decode_batched_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
                                      const void* k, const void* v, float* out, int n_seq, int n_head,
                                      int n_kv_head, int head_dim, int n_pos, int64_t seq_stride);
@@ -235,8 +244,43 @@ int tmac_layer_attention_devpos_kv(tmac_context* ctx, tmac_stream stream, int kv
                                    const float* k_new, const float* v_new, void* k_cache, void* v_cache,
                                    float* out, int n_head, int n_kv_head, int head_dim, const int* pos_dev,
                                    int capacity, float base);
-/* dst[i] = src[i] rounded to nearest even in kv_dtype (BF16 or F16), i < n: fills a 16-bit cache. */
+/* Fills a narrow cache from n fp32 values: BF16 / F16 dst[i] = src[i] rounded to nearest even;
+ * Q8_0 (n % 64 == 0, src 16-byte aligned) n / 64 head rows quantized as the layer step does. */
 int tmac_kv_convert(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* src, void* dst, int64_t n);
+
+/* ---- paged KV caches (extension; the 16-token pages planned at
+ *      LLAMACPP_METAL_STUDY.md:97-101, 155-162) ----
+ * K and V are pools of n_pages pages of 16 rows each (a page = 16 cache rows
+ * of kv_dtype, row layout as above).  block_table [n_seq][max_pages] gives,
+ * for logical page j of sequence s (its rows 16j..16j+15), the pool page that
+ * holds them.  An entry outside [0, n_pages) is clamped into the pool and sets
+ * bit 2 of the device error word.  Pages may be shared between sequences
+ * (a common prefix); the layer step must not write a row another sequence of
+ * the same call reads or writes.
+ *
+ * Decode: sequence s attends its rows 0..lengths[s]-1 (attention_op,
+ * metal_backend.hpp:354, over a paged cache); max_len >= every length and
+ * max_len <= 16 * max_pages (a longer length gives NaN output and bit 1);
+ * total_rows as in tmac_attention_decode_ragged.  A length of 0 gives a zero
+ * output.  q/out [n_seq][n_head][64]. */
+int tmac_attention_decode_paged(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                const void* k_pages, const void* v_pages, int n_pages,
+                                const int32_t* block_table, int max_pages, const int32_t* lengths,
+                                float* out, int n_seq, int n_head, int n_kv_head, int head_dim,
+                                int max_len, int64_t total_rows);
+/* The layer step (tmac_layer_attention) for a batch of sequences on a paged
+ * cache: for each s, with pos = positions[s] (device memory, so a captured step
+ * replays with new positions): RoPE q[s] and k_new[s] at pos, write the rotated
+ * k and v_new[s] to row pos of sequence s (tmac_gguf.cpp:1090-1091), attend
+ * rows 0..pos.  q/out [n_seq][n_head][64], k_new/v_new [n_seq][n_kv_head][64].
+ * max_len >= pos + 1 for every s, max_len <= 16 * max_pages; a position outside
+ * [0, 16 * max_pages) sets bit 0 and skips that sequence, one in
+ * [max_len, 16 * max_pages) gives NaN output and bit 1. */
+int tmac_layer_attention_paged(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                               const float* k_new, const float* v_new, void* k_pages, void* v_pages,
+                               int n_pages, const int32_t* block_table, int max_pages,
+                               const int32_t* positions, float* out, int n_seq, int n_head, int n_kv_head,
+                               int head_dim, int max_len, float base);
 
 /* ---- chunked causal prefill (extension; the reference feeds prompts one token at a time,
  *      tmac_gguf.cpp:1621-1658, so its oracle is attention_op per query row) ----
@@ -275,7 +319,8 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value);
  * (*n_splits = 0 means the head kernel). */
 int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_kv_head, int* split_len,
                      int* n_splits);
-/* Reads and clears the device error word (bit 0: bad device-side position, bit 1: ragged length above max_len).
+/* Reads and clears the device error word (bit 0: bad device-side position, bit 1: ragged or paged length
+ * above max_len, bit 2: block-table entry outside the page pool).
  * Synchronizes the context's device. Returns TMAC_ERR_DEVICE_FAULT if set. */
 int tmac_check_device_error(tmac_context* ctx);
 

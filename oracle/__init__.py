@@ -79,6 +79,14 @@ def _load(path: str) -> ctypes.CDLL:
     lib.oracle_qkv.argtypes = ([ctypes.c_void_p] * 3 + [ctypes.c_int, _F] + [ctypes.c_void_p] * 3 + [_F] * 3 +
                                [ctypes.c_int] * 4)
     lib.oracle_qkv.restype = ctypes.c_int
+    lib.oracle_f32_to_f16_trunc.argtypes = [ctypes.c_float]
+    lib.oracle_f32_to_f16_trunc.restype = ctypes.c_uint16
+    lib.oracle_quantize_q8_0_block.argtypes = [_F, ctypes.c_void_p]
+    lib.oracle_quantize_q8_0_block.restype = None
+    lib.oracle_q8_kv_rows.argtypes = [_F, ctypes.c_int64, ctypes.c_void_p]
+    lib.oracle_q8_kv_rows.restype = None
+    lib.oracle_q8_kv_widen.argtypes = [ctypes.c_void_p, ctypes.c_int64, _F]
+    lib.oracle_q8_kv_widen.restype = None
     _libs[path] = lib
     return lib
 
@@ -253,3 +261,40 @@ def qkv(wq, wk, wv, v_is_q8: bool, x, bq, bk, bv, q_rows: int, k_rows: int, v_ro
     if rc != 0:
         raise ValueError("oracle_qkv: bad arguments")
     return tuple(out)
+
+
+Q8_HEAD_BYTES = 68  # Q8_0 KV head row: int8 q[64], fp16 d0 (dims 0..31), fp16 d1 (dims 32..63)
+
+
+def f32_to_f16_trunc(v: float) -> int:
+    """fp16 bits as scripts/extract_tmac.py:53-74 (float_to_fp16) writes them."""
+    return int(lib().oracle_f32_to_f16_trunc(float(np.float32(v))))
+
+
+def quantize_q8_0_block(x) -> np.ndarray:
+    """32 fp32 values -> the 34-byte Q8_0 block of scripts/extract_tmac.py:159-173."""
+    x = _f32(x)
+    assert x.size == 32
+    out = np.zeros(34, np.uint8)
+    lib().oracle_quantize_q8_0_block(_fp(x), out.ctypes.data)
+    return out
+
+
+def q8_kv_rows(x) -> np.ndarray:
+    """fp32 values (a multiple of 64) -> Q8_0 KV head rows, uint8 [n / 64][68]."""
+    x = _f32(x)
+    assert x.size % 64 == 0
+    n = x.size // 64
+    out = np.zeros((n, Q8_HEAD_BYTES), np.uint8)
+    lib().oracle_q8_kv_rows(_fp(x), n, out.ctypes.data)
+    return out
+
+
+def q8_kv_widen(rows) -> np.ndarray:
+    """Q8_0 KV head rows (uint8, 68 bytes each) -> fp32 [n_head_rows * 64]."""
+    rows = _u8(rows)
+    assert rows.size % Q8_HEAD_BYTES == 0
+    n = rows.size // Q8_HEAD_BYTES
+    out = np.zeros(n * 64, np.float32)
+    lib().oracle_q8_kv_widen(rows.ctypes.data, n, _fp(out))
+    return out

@@ -391,3 +391,73 @@ int oracle_qkv(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int v_is
     if (bv) for (int i = 0; i < v_rows; i++) v[i] += bv[i];
     return 0;
 }
+
+/* ---- Q8_0 requantization ---- */
+
+/* scripts/extract_tmac.py:53-74, bit for bit. */
+uint16_t oracle_f32_to_f16_trunc(float v) {
+    uint32_t bits;
+    memcpy(&bits, &v, 4);
+    if (v == 0.0f) return 0;
+    const uint32_t sign = (bits >> 31) & 1, ex = (bits >> 23) & 0xFF, mant = bits & 0x7FFFFF;
+    if (ex == 0) return 0;
+    uint32_t ex16, mant16;
+    if (ex >= 0x8F) {
+        ex16 = 31;
+        mant16 = 0;
+    } else if (ex <= 0x70) {
+        ex16 = 0;
+        mant16 = 0;
+    } else {
+        ex16 = ex - 127 + 15;
+        mant16 = mant >> 13;
+    }
+    return (uint16_t)((sign << 15) | (ex16 << 10) | mant16);
+}
+
+/* scripts/extract_tmac.py:159-173.  numpy evaluates max_abs / 127.0 and
+ * fp32_block / d either entirely in float32 (numpy >= 2) or as a float64
+ * quotient that is rounded to float32 before use (numpy 1.x value-based
+ * casting); both give the correctly rounded float32 quotient, which is what
+ * the float divisions below compute.  np.round rounds half to even: rintf in
+ * the default rounding mode. */
+void oracle_quantize_q8_0_block(const float* x, uint8_t* block) {
+    float max_abs = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        const float a = fabsf(x[i]);
+        if (a > max_abs) max_abs = a;
+    }
+    const float d = ((double)max_abs < 1e-10) ? 1.0f : max_abs / 127.0f;
+    const uint16_t d_bits = oracle_f32_to_f16_trunc(d);
+    block[0] = (uint8_t)(d_bits & 0xFF);
+    block[1] = (uint8_t)(d_bits >> 8);
+    for (int i = 0; i < 32; i++) {
+        const float q = rintf(x[i] / d);
+        block[2 + i] = (uint8_t)(int8_t)(int)q;
+    }
+}
+
+void oracle_q8_kv_rows(const float* x, int64_t n_head_rows, uint8_t* out) {
+    uint8_t blk[34];
+    for (int64_t r = 0; r < n_head_rows; r++) {
+        uint8_t* o = out + r * 68;
+        for (int b = 0; b < 2; b++) {
+            oracle_quantize_q8_0_block(x + r * 64 + 32 * b, blk);
+            memcpy(o + 32 * b, blk + 2, 32);
+            o[64 + 2 * b] = blk[0];
+            o[65 + 2 * b] = blk[1];
+        }
+    }
+}
+
+void oracle_q8_kv_widen(const uint8_t* rows, int64_t n_head_rows, float* out) {
+    for (int64_t r = 0; r < n_head_rows; r++) {
+        const uint8_t* o = rows + r * 68;
+        for (int e = 0; e < 64; e++) {
+            const int b = e / 32;
+            const float scale = oracle_f16_to_f32((uint16_t)(o[64 + 2 * b] | (o[65 + 2 * b] << 8)));
+            const int8_t val = (int8_t)o[e];
+            out[r * 64 + e] = val * scale;
+        }
+    }
+}

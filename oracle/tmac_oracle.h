@@ -17,6 +17,7 @@
  *   Q6_K / Q4_K   tmac_gguf.cpp:330-397    (dequant_q6_k / dequant_q4_k)
  *   matmul        tmac_gguf.cpp:405-414, 510-514 (read_tensor + the CPU row loop)
  *   QKV + bias    tmac_gguf.cpp:1046-1081  (three matmuls on the normed hidden state, then bias adds)
+ *   Q8_0 requant  scripts/extract_tmac.py:53-74, 159-173 (float_to_fp16, quantize_q8_0_block)
  *
  * Generalisations (the reference hard-codes them): n_head / n_kv_head /
  * head_dim / base are arguments, the score buffer is sized by n_pos instead of
@@ -117,6 +118,21 @@ int oracle_matmul_q(int type, const uint8_t* w, const float* x, float* y, int ro
 int oracle_qkv(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, int v_is_q8, const float* x,
                const float* bq, const float* bk, const float* bv, float* q, float* k, float* v,
                int q_rows, int k_rows, int v_rows, int cols);
+
+/* ---- Q8_0 requantization (the Q8_0 KV cache) ----
+ * scripts/extract_tmac.py:53-74 float_to_fp16: sign, exponent rebased
+ * (exp - 127 + 15), mantissa truncated to 10 bits; 0 and fp32-subnormal
+ * inputs give 0, fp32 exponents <= 0x70 give a signed zero, >= 0x8F infinity. */
+uint16_t oracle_f32_to_f16_trunc(float v);
+/* scripts/extract_tmac.py:159-173 quantize_q8_0_block: max_abs = max |x|,
+ * d = 1 if max_abs < 1e-10 else max_abs / 127, q = round(x / d) half to even
+ * (numpy), block = fp16 d (float_to_fp16) then int8 q[32]: 34 bytes. */
+void oracle_quantize_q8_0_block(const float* x, uint8_t* block);
+/* Q8_0 KV cache head rows (68 bytes per 64 values): the two blocks of each
+ * 64 values regrouped as q[0..63], d0, d1. */
+void oracle_q8_kv_rows(const float* x, int64_t n_head_rows, uint8_t* out);
+/* Head rows -> fp32 with dequant_q8_0 (tmac_gguf.cpp:240-250): value = q * d. */
+void oracle_q8_kv_widen(const uint8_t* rows, int64_t n_head_rows, float* out);
 
 #ifdef __cplusplus
 }

@@ -169,7 +169,7 @@ def test_graph_replay_16bit(ctx, dt):
 
 def test_rejects_bad_kv_dtype(ctx):
     d = ctx.empty(NH * HD * 4)
-    assert ctx.decode_batched(d, d, d, d, 1, NH, NKV, HD, 2, 2, kv_dtype=3, check=False) == \
+    assert ctx.decode_batched(d, d, d, d, 1, NH, NKV, HD, 2, 2, kv_dtype=4, check=False) == \
         tmac_attn.TMAC_ERR_INVALID_ARG
     assert ctx.kv_convert(tmac_attn.TMAC_KV_F32, d, d, 4, check=False) == tmac_attn.TMAC_ERR_INVALID_ARG
 

@@ -12,6 +12,10 @@ constexpr int kSlotsPerWave = 8;    // 64 lanes = 8 (row, kv-head) slots x 8 dim
 constexpr int kGroupWaves = 8;      // "group" decode kernel: 512 threads per workgroup
 constexpr int kPrefetchDepth = 3;   // group kernel: steps of K/V in flight per wave (191 VGPRs at G = 7)
 constexpr int kPrefetchDepth16 = 6; // the same for 16-bit caches: half the bytes per step, twice the steps
+constexpr int kPrefetchDepthQ8 = 8; // the same for Q8_0 caches (136-byte rows at 2 kv heads)
+constexpr int kQ8HeadBytes = 68;    // Q8_0 cache: one (row, kv head) = int8 q[64] + fp16 d0, d1
+constexpr int kPageRows = 16;       // paged caches: rows per page
+constexpr int kPageShift = 4;       // log2(kPageRows)
 constexpr int kHeadWaves = 16;      // "head" decode kernel (short contexts): 1024 threads
 constexpr int kHeadPrefetchDepth = 2;
 constexpr int kMaxSplits = 256;     // split-KV workgroups per sequence, at most
@@ -21,7 +25,7 @@ constexpr int kPartialStride = kHeadDim + 2;  // per (split, head): acc[64], m, 
 // row = [n_kv_head][64] fp32 (tmac_gguf.cpp:200-201).
 struct DecodeArgs {
     const float* q;          // [n_seq][n_head][64]; layer mode: pre-RoPE q of one token
-    const float* k;          // cache / pool base
+    const float* k;          // cache / pool base (element type per kernel: fp32, bf16, fp16, Q8_0)
     const float* v;
     float* out;              // [n_seq][n_head][64]
     const int64_t* offsets;  // ragged mode: first row of each sequence in the pool
@@ -45,8 +49,14 @@ struct DecodeArgs {
     const int* pos_dev;      // device-side position (graph replay); null -> pos_host
     int pos_host;
     int rope_rows;
-    int capacity;            // rows in the layer cache
-    int* err;                // device error word (bit 0: position out of range)
+    int capacity;            // rows in the layer cache (paged layer mode: max_pages * kPageRows)
+    int* err;                // device error word (bit 0: position out of range, bit 1: length above
+                             // the launch's max_len, bit 2: block-table entry outside the pool)
+    // paged modes: the caches are pools of kPageRows-row pages
+    const int32_t* block_table;  // [n_seq][max_pages]: pool page of each sequence's logical page
+    const int32_t* positions;    // paged layer mode: [n_seq] position of each sequence's new token
+    int max_pages;
+    int n_pages;                 // pages in each pool
 };
 
 // Chunked causal prefill: query i of sequence s sits at absolute position
@@ -93,7 +103,7 @@ struct CvtArgs {
     const float* src;
     void* dst;
     int64_t n;
-    int dtype;               // 1: bf16, 2: fp16
+    int dtype;               // 1: bf16, 2: fp16 (tmac_cvt16; tmac_cvt_q8 ignores it)
 };
 
 // QKV projection of one layer: y[s] = W[s] x (+ bias[s]) for s = q, k, v.

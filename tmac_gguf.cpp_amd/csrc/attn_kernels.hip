@@ -43,7 +43,9 @@ constexpr int kLanesPerSlot = 8;
 constexpr int kDimsPerLane = kHeadDim / kLanesPerSlot;  // 8
 constexpr int kSlots = 64 / kLanesPerSlot;              // 8 (row, kv) slots per wave step
 
-enum Mode { kUniform = 0, kRagged = 1, kLayer = 2 };
+enum Mode { kUniform = 0, kRagged = 1, kLayer = 2, kPaged = 3, kPagedLayer = 4 };
+constexpr bool is_layer(int m) { return m == kLayer || m == kPagedLayer; }
+constexpr bool is_paged(int m) { return m == kPaged || m == kPagedLayer; }
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -118,6 +120,184 @@ __device__ __forceinline__ void round8(float (&x)[8], const T*) {
     for (int t = 0; t < 8; ++t) x[t] = (float)(T)x[t];
 }
 
+__device__ __forceinline__ float half_bits_to_float(unsigned h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+}
+
+// Q8_0 cache (TMAC_KV_Q8_0).  The 64 dims of one (row, kv head) form a
+// 68-byte "head row": int8 q[64], then the fp16 scales d0 (dims 0..31) and d1
+// (dims 32..63).  Those are the two 34-byte GGML Q8_0 blocks of the 64 dims
+// (value = q * d, as dequant_q8_0 reads them, tmac_gguf.cpp:240-250) with the
+// scales moved behind the values, so each lane's 4-dim runs are aligned
+// 4-byte words.
+struct q8_0_t {};
+
+// Byte geometry of one head row of a cache of element type T.
+template <typename T>
+struct CacheFmt {
+    static constexpr int kHeadBytes = kHeadDim * (int)sizeof(T);
+    static constexpr int kDimBytes = (int)sizeof(T);
+};
+template <>
+struct CacheFmt<q8_0_t> {
+    static constexpr int kHeadBytes = kQ8HeadBytes;
+    static constexpr int kDimBytes = 1;
+};
+
+// This lane's 8 dims of a cache head row as loaded (raw words): fp32 8
+// floats, 16-bit 4 words, Q8_0 the two 4-byte runs plus the scale word.
+// Prefetch buffers hold raw rows and are widened where they are used, so the
+// wait for a load sits at its use, not right behind the load.
+template <typename T>
+struct RawRow {
+    unsigned w[sizeof(T) == 2 ? 4 : 3];
+};
+template <>
+struct RawRow<float> {
+    float w[8];
+};
+
+// p points at the lane's dim 4c of a head row.
+template <typename T>
+__device__ __forceinline__ void load_raw(RawRow<T>& r, const char* p, int c) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    if constexpr (sizeof(T) == 4) {
+        load8(r.w, reinterpret_cast<const float*>(p));
+    } else if constexpr (sizeof(T) == 2) {
+        const u32x2 a = *reinterpret_cast<const u32x2*>(p);
+        const u32x2 b = *reinterpret_cast<const u32x2*>(p + 32 * sizeof(T));
+        r.w[0] = a[0];
+        r.w[1] = a[1];
+        r.w[2] = b[0];
+        r.w[3] = b[1];
+    } else {
+        r.w[0] = *reinterpret_cast<const unsigned*>(p);            // dims 4c..4c+3
+        r.w[1] = *reinterpret_cast<const unsigned*>(p + 32);       // dims 32+4c..32+4c+3
+        r.w[2] = *reinterpret_cast<const unsigned*>(p + 64 - 4 * c);  // d0 | d1 << 16
+    }
+}
+
+// Raw row -> fp32, exactly.
+template <typename T>
+__device__ __forceinline__ void widen(float (&x)[8], const RawRow<T>& r) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x[t] = r.w[t];
+    } else if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if constexpr (__is_same(T, __bf16)) {
+                x[2 * t] = __builtin_bit_cast(float, r.w[t] << 16);
+                x[2 * t + 1] = __builtin_bit_cast(float, r.w[t] & 0xFFFF0000u);
+            } else {
+                x[2 * t] = half_bits_to_float(r.w[t] & 0xFFFFu);
+                x[2 * t + 1] = half_bits_to_float(r.w[t] >> 16);
+            }
+        }
+    } else {
+        const float d0 = half_bits_to_float(r.w[2] & 0xFFFFu), d1 = half_bits_to_float(r.w[2] >> 16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            x[t] = (float)(signed char)(r.w[0] >> (8 * t)) * d0;  // |q| <= 127, 11-bit d: exact product
+            x[4 + t] = (float)(signed char)(r.w[1] >> (8 * t)) * d1;
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void load_row(float (&x)[8], const char* p, int c) {
+    RawRow<T> r;
+    load_raw<T>(r, p, c);
+    widen<T>(x, r);
+}
+
+// fp16 bits of a Q8_0 scale exactly as the reference's converter writes them
+// (scripts/extract_tmac.py:53-74): exponent rebased, mantissa truncated to 10
+// bits, magnitudes below fp16's normal range flushed to 0, exponents above
+// its range turned into infinity.
+__device__ __forceinline__ unsigned f16_bits_trunc(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const unsigned e = (u >> 23) & 0xFFu;
+    if ((u & 0x7FFFFFFFu) == 0 || e == 0) return 0;
+    const unsigned s = (u >> 31) << 15;
+    if (e >= 0x8Fu) return s | (31u << 10);
+    if (e <= 0x70u) return s;
+    return s | ((e - 112u) << 10) | ((u & 0x7FFFFFu) >> 13);
+}
+
+// One lane's 4 dims of a 32-dim block quantized as quantize_q8_0_block does
+// (scripts/extract_tmac.py:159-173): d = amax / 127 (1 when amax < 1e-10),
+// q = x / d rounded half to even, the scale stored as f16_bits_trunc(d).
+// amax is the block's max |x|.  Returns the 4 bytes; x becomes what the cache
+// then holds, q * fp16(d).
+__device__ __forceinline__ unsigned quant4(float* x, float amax, unsigned& dbits) {
+    const float d = amax < 1e-10f ? 1.0f : amax / 127.0f;  // IEEE division (hipcc default)
+    dbits = f16_bits_trunc(d);
+    const float dq = half_bits_to_float(dbits);
+    unsigned packed = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int qv = (int)__builtin_rintf(x[t] / d);
+        packed |= ((unsigned)qv & 0xFFu) << (8 * t);
+        x[t] = (float)qv * dq;
+    }
+    return packed;
+}
+
+// Rounds x (this lane's 8 dims of a new cache head row) to the value a cache
+// of type T holds and, if `store`, writes it at p (the lane's dim 4c).
+template <typename T>
+__device__ __forceinline__ void put_row(float (&x)[8], char* p, int, bool store) {
+    round8(x, static_cast<const T*>(nullptr));
+    if (store) store8(reinterpret_cast<T*>(p), x);
+}
+// Q8_0: the 8 lanes of a slot hold the head row's 64 dims and must all call
+// (the block maxima are reduced across them); lane 0 writes the scales.
+template <>
+__device__ __forceinline__ void put_row<q8_0_t>(float (&x)[8], char* p, int c, bool store) {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        a0 = fmaxf(a0, fabsf(x[t]));
+        a1 = fmaxf(a1, fabsf(x[4 + t]));
+    }
+#pragma unroll
+    for (int mask = 1; mask < kLanesPerSlot; mask <<= 1) {
+        a0 = fmaxf(a0, __shfl_xor(a0, mask));
+        a1 = fmaxf(a1, __shfl_xor(a1, mask));
+    }
+    unsigned d0, d1;
+    const unsigned lo = quant4(x, a0, d0);
+    const unsigned hi = quant4(x + 4, a1, d1);
+    if (store) {
+        *reinterpret_cast<unsigned*>(p) = lo;
+        *reinterpret_cast<unsigned*>(p + 32) = hi;
+        if (c == 0) *reinterpret_cast<unsigned*>(p + 64) = d0 | (d1 << 16);
+    }
+}
+
+// Paged modes: a sequence's rows live in kPageRows-row pages of a pool, and
+// table[j] is the pool page holding its rows kPageRows*j .. kPageRows*j + 15.
+// Page indices outside [0, n_pages) are clamped into the pool and reported.
+struct PageMap {
+    const int32_t* table;  // this sequence's block-table row
+    int r0;                // first row of the range being attended (a multiple of kPageRows)
+    int n_pages;
+};
+
+typedef __attribute__((address_space(4))) const int32_t* const_i32_ptr;
+
+// Pool page of a sequence row (wave-uniform).  The block table is read-only
+// for the kernel's lifetime, so it is read through the constant address space
+// (a scalar load); a vector load would join the in-order queue of the K/V
+// prefetches and wait behind them.
+__device__ __forceinline__ unsigned page_of(const PageMap& pm, int row, unsigned& bad) {
+    row = __builtin_amdgcn_readfirstlane(row);  // uniform by construction; lets the load be scalar
+    const unsigned pg = (unsigned)((const_i32_ptr)pm.table)[row >> kPageShift];
+    bad |= pg >= (unsigned)pm.n_pages ? 1u : 0u;
+    return min(pg, (unsigned)pm.n_pages - 1u);
+}
+
 // RoPE on a lane's 8 dims.  Pairs (d, d+1), d even, never straddle a lane:
 // dims 4c..4c+3 are pairs 2c, 2c+1 and dims 32+4c.. are pairs 16+2c, 17+2c.
 __device__ __forceinline__ void rope8(float (&x)[8], const float2* __restrict__ cs_row, int c) {
@@ -190,19 +370,23 @@ __device__ __forceinline__ void attend(const float (&q)[G][kDimsPerLane], State<
 }
 
 // Attends this wave's share of `n_rows` cache rows starting at kb/vb.  A step
-// covers PPS = 8/KVS rows x KVS kv heads (ROW floats between rows).  Steps are
+// covers PPS = 8/KVS rows x KVS kv heads (ROWB bytes between rows).  Steps are
 // dealt round-robin to the NW waves of the workgroup (the workgroup streams its
 // range front to back); DEPTH steps of K/V are kept in flight per wave.  Full
 // steps run in the main loop; the one partial step at the end of the range (if
 // any) is loaded and masked after it, so the loop body holds a single copy of
-// the softmax state.
-template <typename T, int G, int KVS, int ROW, int NW, int DEPTH>
-__device__ __forceinline__ void attend_rows(const T* __restrict__ kb, const T* __restrict__ vb,
+// the softmax state.  PAGED: kb/vb are the pool bases and pm maps rows to
+// pages (PPS divides kPageRows and pm.r0 is page-aligned, so a step never
+// straddles a page).
+template <typename T, int G, int KVS, int ROWB, int NW, int DEPTH, bool PAGED>
+__device__ __forceinline__ void attend_rows(const char* __restrict__ kb, const char* __restrict__ vb,
                                             int n_rows, int wave, int lane_off, int lane_row,
-                                            int lane_col, const float (&q)[G][kDimsPerLane], State<G>& st,
-                                            int rot, bool blocked) {
+                                            int lane_col, int c, const float (&q)[G][kDimsPerLane],
+                                            State<G>& st, int rot, bool blocked, const PageMap& pm,
+                                            unsigned& bad) {
     constexpr int PPS = kSlots / KVS;   // rows per step
-    constexpr int STEP = PPS * ROW;     // floats between consecutive steps
+    constexpr int STEP = PPS * ROWB;    // bytes between consecutive steps
+    static_assert(kPageRows % PPS == 0, "a step must not straddle a page");
     const int full = n_rows / PPS;      // steps whose rows are all in range
     // Interleaved: wave w takes steps w, w + NW, ...  Blocked: wave w takes a
     // contiguous run of steps (NW independent streams per workgroup).
@@ -223,40 +407,60 @@ __device__ __forceinline__ void attend_rows(const T* __restrict__ kb, const T* _
         // concurrently running workgroups stream from staggered offsets of their
         // ranges (spreads the HBM channels; the merge is order-independent).
         rot %= nk;
-        float kbuf[DEPTH][kDimsPerLane], vbuf[DEPTH][kDimsPerLane];
-        const T* kp = kb + (size_t)first * STEP + lane_off;
-        const T* vp = vb + (size_t)first * STEP + lane_off;
-        auto at = [&](int k) {
+        RawRow<T> kbuf[DEPTH], vbuf[DEPTH];
+        const char* kp = kb + (PAGED ? 0 : (size_t)first * STEP) + lane_off;
+        const char* vp = vb + (PAGED ? 0 : (size_t)first * STEP) + lane_off;
+        auto at = [&](int k) -> size_t {
             int kk = k + rot;
             kk -= (kk >= nk) ? nk : 0;
-            return (size_t)kk * stride * STEP;
+            if (!PAGED) return (size_t)kk * stride * STEP;
+            const int row = pm.r0 + (first + kk * stride) * PPS;
+            return ((size_t)page_of(pm, row, bad) * kPageRows + (row & (kPageRows - 1))) * ROWB;
         };
         // Prefetches are unconditional (indices past the wave's last step are
         // clamped to it, an L2 hit), so every buffer keeps one register
         // assignment across iterations; a conditional load would make the
         // compiler rotate buffers with copies, which must first wait for all
         // loads in flight.
+        // Narrow caches: the prologue issues step 0 first, then step 1, ...
+        // (the scheduling barrier keeps that order).  The wait at the loop
+        // head covers both the loop entry and the back edge, so with another
+        // prologue order the entry path forces a wait for (nearly) every load
+        // in flight on every iteration (4% slower at config 3 with a bf16
+        // cache).  The fp32 kernel measured 1% faster without the barrier.
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            load8(kbuf[d], kp + at(min(d, nk - 1)));
-            load8(vbuf[d], vp + at(min(d, nk - 1)));
+            load_raw<T>(kbuf[d], kp + at(min(d, nk - 1)), c);
+            load_raw<T>(vbuf[d], vp + at(min(d, nk - 1)), c);
+            if constexpr (sizeof(T) < sizeof(float)) __builtin_amdgcn_sched_barrier(0);
         }
         for (int k0 = 0; k0 < nk; k0 += DEPTH) {
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
-                if (k0 + d < nk) attend<G, KVS, false>(q, st, kbuf[d], vbuf[d], true);
+                if (k0 + d < nk) {
+                    float kf[kDimsPerLane], vf[kDimsPerLane];
+                    widen<T>(kf, kbuf[d]);
+                    widen<T>(vf, vbuf[d]);
+                    attend<G, KVS, false>(q, st, kf, vf, true);
+                }
                 const int kn = min(k0 + d + DEPTH, nk - 1);
-                load8(kbuf[d], kp + at(kn));
-                load8(vbuf[d], vp + at(kn));
+                load_raw<T>(kbuf[d], kp + at(kn), c);
+                load_raw<T>(vbuf[d], vp + at(kn), c);
             }
         }
     }
     if (full * PPS < n_rows && (full % NW) == wave) {
         const int row = full * PPS + lane_row;
-        const int off = min(row, n_rows - 1) * ROW + lane_col;
+        const int r = min(row, n_rows - 1);  // in the same step (and page) as row full * PPS
+        size_t off;
+        if (PAGED)
+            off = ((size_t)page_of(pm, pm.r0 + full * PPS, bad) * kPageRows + ((pm.r0 + r) & (kPageRows - 1))) *
+                      ROWB + lane_col;
+        else
+            off = (size_t)r * ROWB + lane_col;
         float kf[kDimsPerLane], vf[kDimsPerLane];
-        load8(kf, kb + off);
-        load8(vf, vb + off);
+        load_row<T>(kf, kb + off, c);
+        load_row<T>(vf, vb + off, c);
         attend<G, KVS, true>(q, st, kf, vf, row < n_rows);
     }
 }
@@ -325,45 +529,48 @@ __device__ __forceinline__ void finish(State<G>& st, int lane, int wave, bool di
     }
 }
 
-// Rows attended by sequence `seq` (n_pos) and its cache base, per mode.
-// Returns false for an out-of-range device position.
-template <int KV, int MODE>
+// Rows attended by sequence `seq` (n_pos) and its first cache row (base;
+// 0 in the layer and paged modes), per mode.  Returns false for an
+// out-of-range position.
+template <int MODE>
 __device__ __forceinline__ bool seq_geometry(const DecodeArgs& a, int seq, int& n_pos, int& pos,
                                              size_t& base) {
-    constexpr int ROW = KV * kHeadDim;
     pos = 0;
+    base = 0;
     if (MODE == kUniform) {
         n_pos = a.n_pos;
-        base = (size_t)seq * (size_t)a.seq_stride * ROW;
+        base = (size_t)seq * (size_t)a.seq_stride;
     } else if (MODE == kRagged) {
         n_pos = a.lengths[seq];
-        base = (size_t)a.offsets[seq] * ROW;
+        base = (size_t)a.offsets[seq];
+    } else if (MODE == kPaged) {
+        n_pos = a.lengths[seq];
     } else {
-        pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+        pos = MODE == kPagedLayer ? a.positions[seq] : (a.pos_dev ? *a.pos_dev : a.pos_host);
         if (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) return false;
         n_pos = pos + 1;
-        base = 0;
     }
     return true;
 }
 
-// Ragged group kernel: flat unit index -> (sequence, split).  Sequence s owns
+// Flat unit grid (ragged and paged modes): unit index -> (sequence, split).
+// Sequence s with L_s = lengths[s] + add rows owns
 // clamp(ceil(L_s / split_len), 1, n_splits) consecutive units (a length above
 // the launch's max_len still gets its units, whose first one reports it), so
 // the unit count never exceeds the n_seq * n_splits grid; the units that carry
 // rows fill the front of the grid (round-robin dispatch then spreads them
 // evenly over the XCDs) and surplus workgroups at the end exit.  Every wave
 // computes the same answer with a 64-lane inclusive scan per 64 sequences.
-__device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths, int n_seq, int split_len,
-                                            int n_splits, int unit, int& seq, int& split) {
+__device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths, int add, int n_seq,
+                                            int split_len, int n_splits, int unit, int& seq, int& split) {
     const int lane = threadIdx.x & 63;
     int base = 0;
     for (int c0 = 0; c0 < n_seq; c0 += 64) {
         const int sq = c0 + lane;
         int u = 0;
         if (sq < n_seq) {
-            const int len = lengths[sq];
-            u = len > 0 ? min((len + split_len - 1) / split_len, n_splits) : 1;
+            const long long len = (long long)lengths[sq] + add;
+            u = len > 0 ? (int)min((len + split_len - 1) / split_len, (long long)n_splits) : 1;
         }
         int incl = u;
 #pragma unroll
@@ -371,7 +578,7 @@ __device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths,
             const int t = __shfl_up(incl, off);
             if (lane >= off) incl += t;
         }
-        const int total = __shfl(incl, 63);
+        const int total = __builtin_amdgcn_readfirstlane(__shfl(incl, 63));  // uniform: keeps the loop's branches scalar
         if (unit < base + total) {
             const unsigned long long hit = __ballot(unit < base + incl);
             const int first = __ffsll((long long)hit) - 1;
@@ -391,27 +598,41 @@ __device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths,
 //   PER_HEAD = true ("head" kernel, short contexts): grid (q head, seq), one
 //     split; the workgroup attends all rows for one query head, reading only
 //     its kv head's 256-byte half rows, so no cross-workgroup merge is needed.
+// Ragged and paged modes launch a flat unit grid instead of (split, seq).
+// The paged layer mode is the layer step of a batch: sequence s's new token
+// sits at positions[s], and its q/k_new/v_new rows are the s-th of each input.
 template <typename T, int G, int KV, int NW, int DEPTH, int MODE, bool PER_HEAD>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
-    constexpr int ROW = KV * kHeadDim;
+    constexpr int HB = CacheFmt<T>::kHeadBytes;
+    constexpr int ROWB = KV * HB;            // cache bytes per row
+    constexpr int ROWF = KV * kHeadDim;      // floats per k_new / v_new row
     constexpr int NH = KV * G;
     constexpr int KVS = PER_HEAD ? 1 : KV;  // kv heads per step
     constexpr int GW = PER_HEAD ? 1 : G;    // query heads per lane
+    constexpr bool PAGED = is_paged(MODE);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int split = PER_HEAD ? 0 : blockIdx.x;
     const int head = PER_HEAD ? blockIdx.x : 0;
     int seq = blockIdx.y;
-    if (MODE == kRagged && !PER_HEAD) {  // grid = flat list of (sequence, split) units
-        if (!ragged_unit(a.lengths, a.n_seq, a.split_len, a.n_splits, blockIdx.x, seq, split)) return;
+    if ((MODE == kRagged || PAGED) && !PER_HEAD) {  // grid = flat list of (sequence, split) units
+        const bool by_pos = MODE == kPagedLayer;
+        if (!ragged_unit(by_pos ? a.positions : a.lengths, by_pos ? 1 : 0, a.n_seq, a.split_len, a.n_splits,
+                         blockIdx.x, seq, split))
+            return;
     }
 
     int n_pos, pos;
     size_t base;
-    if (!seq_geometry<KV, MODE>(a, seq, n_pos, pos, base)) {
-        if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
+    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) {
+        if (split == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
         return;
     }
+    // Per-sequence values are uniform; read from memory (ragged, paged modes)
+    // they would otherwise stay in vector registers, and so would all the
+    // address arithmetic derived from them.
+    n_pos = __builtin_amdgcn_readfirstlane(n_pos);
+    pos = __builtin_amdgcn_readfirstlane(pos);
     float* out_seq = a.out + (size_t)seq * NH * kHeadDim;
     float* out_heads = out_seq + (PER_HEAD ? head * kHeadDim : 0);
     if (n_pos <= 0) {  // ragged sequence with no rows: defined as a zero output
@@ -420,7 +641,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         return;
     }
     const int n_act = (n_pos + a.split_len - 1) / a.split_len;
-    if (n_act > a.n_splits) {  // ragged length above the max_len the grid was sized for
+    if (n_act > a.n_splits) {  // length above the max_len the grid was sized for
         if (split == 0) {
             for (int i = threadIdx.x; i < KVS * GW * kHeadDim; i += NW * 64) out_heads[i] = __builtin_nanf("");
             if (threadIdx.x == 0) atomicOr(a.err, 2);
@@ -428,58 +649,62 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         return;
     }
     if (split >= n_act) return;
-    const int mem_rows = (MODE == kLayer) ? pos : n_pos;  // layer mode: row `pos` comes from registers
+    const int mem_rows = is_layer(MODE) ? pos : n_pos;  // layer modes: row `pos` comes from registers
     const int r0 = split * a.split_len;
     const int r1 = min(r0 + a.split_len, mem_rows);
 
     const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
     const int lane_row = slot / KVS;
     const int kvh = PER_HEAD ? head / G : slot % KVS;  // kv head this lane reads
-    const int lane_col = kvh * kHeadDim + 4 * c;
-    const int lane_off = lane_row * ROW + lane_col;
+    const int lane_colf = kvh * kHeadDim + 4 * c;                     // in fp32 inputs
+    const int lane_col = kvh * HB + 4 * c * CacheFmt<T>::kDimBytes;   // in a cache row (bytes)
+    const int lane_off = lane_row * ROWB + lane_col;
 
     // Query of this lane's GW heads (its 8 dims), pre-scaled for base-2 softmax.
     float q[GW][kDimsPerLane];
     const float2* cs_row = nullptr;
-    if (MODE == kLayer) cs_row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
+    if (is_layer(MODE)) cs_row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
         const int qh = PER_HEAD ? head : kvh * G + g;
         load8(q[g], a.q + ((size_t)seq * NH + qh) * kHeadDim + 4 * c);
-        if (MODE == kLayer) rope8(q[g], cs_row, c);
+        if (is_layer(MODE)) rope8(q[g], cs_row, c);
 #pragma unroll
         for (int t = 0; t < kDimsPerLane; ++t) q[g][t] *= a.qscale;
     }
 
     State<GW> st;
     state_init(st);
-    const T* kseq = reinterpret_cast<const T*>(a.k) + base;
-    const T* vseq = reinterpret_cast<const T*>(a.v) + base;
-    attend_rows<T, GW, KVS, ROW, NW, DEPTH>(kseq + (size_t)r0 * ROW, vseq + (size_t)r0 * ROW, max(r1 - r0, 0),
-                                         wave, lane_off, lane_row, lane_col, q, st,
-                                         (blockIdx.y * gridDim.x + blockIdx.x) * a.rot_mul, a.blocked != 0);
+    const char* kc = reinterpret_cast<const char*>(a.k) + (PAGED ? 0 : (base + r0) * ROWB);
+    const char* vc = reinterpret_cast<const char*>(a.v) + (PAGED ? 0 : (base + r0) * ROWB);
+    const PageMap pm{PAGED ? a.block_table + (size_t)seq * a.max_pages : nullptr, r0, a.n_pages};
+    unsigned bad = 0;
+    attend_rows<T, GW, KVS, ROWB, NW, DEPTH, PAGED>(kc, vc, max(r1 - r0, 0), wave, lane_off, lane_row, lane_col, c,
+                                                   q, st, (blockIdx.y * gridDim.x + blockIdx.x) * a.rot_mul,
+                                                   a.blocked != 0, pm, bad);
 
-    if (MODE == kLayer && split == n_act - 1 && wave == 0) {
+    if (is_layer(MODE) && split == n_act - 1 && wave == 0) {
         // The new token (row `pos`): RoPE its k, write k/v to the cache row
         // (tmac_gguf.cpp:1090-1091, once per kv head) and attend it from registers.
         const bool mine = (lane_row == 0);
         float kf[kDimsPerLane], vf[kDimsPerLane];
         if (mine) {
-            load8(kf, a.k_new + lane_col);
-            load8(vf, a.v_new + lane_col);
+            const size_t in = (MODE == kPagedLayer ? (size_t)seq * ROWF : 0) + lane_colf;
+            load8(kf, a.k_new + in);
+            load8(vf, a.v_new + in);
             rope8(kf, cs_row, c);
-            round8(kf, kseq);
-            round8(vf, kseq);
-            if (!PER_HEAD || head % G == 0) {
-                store8(reinterpret_cast<T*>(a.k_out) + (size_t)pos * ROW + lane_col, kf);
-                store8(reinterpret_cast<T*>(a.v_out) + (size_t)pos * ROW + lane_col, vf);
-            }
+            size_t row = (size_t)pos;
+            if (PAGED) row = (size_t)page_of(pm, pos, bad) * kPageRows + (pos & (kPageRows - 1));
+            const bool store = !PER_HEAD || head % G == 0;
+            put_row<T>(kf, reinterpret_cast<char*>(a.k_out) + row * ROWB + lane_col, c, store);
+            put_row<T>(vf, reinterpret_cast<char*>(a.v_out) + row * ROWB + lane_col, c, store);
         } else {
 #pragma unroll
             for (int t = 0; t < kDimsPerLane; ++t) kf[t] = vf[t] = 0.f;
         }
         attend<GW, KVS, true>(q, st, kf, vf, mine);
     }
+    if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
 
     const bool direct = (n_act == 1);
     float* ws_split = direct ? nullptr : a.ws + ((size_t)seq * a.n_splits + split) * NH * kPartialStride;
@@ -497,17 +722,20 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 // softmax state and stale rows past the length never reach the sums.
 template <typename T, int G, int KV, int NW, int DEPTH, int MODE>
 __device__ __forceinline__ void head_body(const DecodeArgs& a) {
-    constexpr int ROW = KV * kHeadDim;
+    static_assert(!is_paged(MODE), "the head kernel has no paged modes");
+    constexpr int HB = CacheFmt<T>::kHeadBytes;
+    constexpr int ROWB = KV * HB;    // cache bytes per row
     constexpr int NH = KV * G;
     constexpr int PPS = kSlots;      // rows per step (one kv head)
-    constexpr int STEP = PPS * ROW;
+    constexpr int STEP = PPS * ROWB;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int head = blockIdx.x, seq = blockIdx.y;
     const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
     const int kvh = head / G;
-    const int lane_col = kvh * kHeadDim + 4 * c;
-    const int lane_off = slot * ROW + lane_col;
+    const int lane_colf = kvh * kHeadDim + 4 * c;                     // in fp32 inputs
+    const int lane_col = kvh * HB + 4 * c * CacheFmt<T>::kDimBytes;   // in a cache row (bytes)
+    const int lane_off = slot * ROWB + lane_col;
 
     // 1. loads that do not depend on the length
     float q[1][kDimsPerLane];
@@ -515,34 +743,37 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     float kn[kDimsPerLane], vn[kDimsPerLane];
     const bool new_lane = (MODE == kLayer) && wave == 0 && slot == 0;
     if (new_lane) {
-        load8(kn, a.k_new + lane_col);
-        load8(vn, a.v_new + lane_col);
+        load8(kn, a.k_new + lane_colf);
+        load8(vn, a.v_new + lane_colf);
     }
-    size_t base = 0;
-    int bound;  // rows that may be loaded
+    size_t base = 0;  // first cache row of the sequence
+    int bound;        // rows that may be loaded
     if (MODE == kUniform) {
-        base = (size_t)seq * (size_t)a.seq_stride * ROW;
+        base = (size_t)seq * (size_t)a.seq_stride;
         bound = a.n_pos;
     } else if (MODE == kRagged) {
-        base = (size_t)a.offsets[seq] * ROW;
+        base = (size_t)a.offsets[seq];
         bound = a.lengths[seq];
     } else {
         bound = a.capacity;
     }
-    const T* kb = reinterpret_cast<const T*>(a.k) + base + wave * STEP + lane_off;
-    const T* vb = reinterpret_cast<const T*>(a.v) + base + wave * STEP + lane_off;
-    auto row_off = [&](int k) {  // float offset (from kb) of this lane's row in the wave's k-th step
+    const char* kb = reinterpret_cast<const char*>(a.k) + base * ROWB + wave * STEP + lane_off;
+    const char* vb = reinterpret_cast<const char*>(a.v) + base * ROWB + wave * STEP + lane_off;
+    // Byte offset (from kb) of this lane's row in the wave's k-th step, rows
+    // clamped below `lim`.
+    auto row_off = [&](int k, int lim) {
         const int row = (wave + NW * k) * PPS + slot;
-        const int r = min(row, bound - 1);
-        return (ptrdiff_t)(r - wave * PPS - slot) * ROW;
+        const int r = min(row, lim - 1);
+        return (ptrdiff_t)(r - wave * PPS - slot) * ROWB;
     };
     // Step 0 of every wave is loaded speculatively (rows < bound are allocated);
     // later steps wait for the length so short contexts do not pull the whole
     // allocation through the CU.
-    float kbuf[DEPTH][kDimsPerLane], vbuf[DEPTH][kDimsPerLane];
-    if (bound > 0) {
-        load8(kbuf[0], kb + row_off(0));
-        load8(vbuf[0], vb + row_off(0));
+    RawRow<T> kbuf[DEPTH], vbuf[DEPTH];
+    // (bound >= 1 except for an empty ragged sequence.)
+    if (MODE != kRagged || bound > 0) {
+        load_raw<T>(kbuf[0], kb + row_off(0, bound), c);
+        load_raw<T>(vbuf[0], vb + row_off(0, bound), c);
     }
 
     // 2. the attended length
@@ -583,26 +814,32 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     state_init(st);
     const int n_steps = (mem_rows + PPS - 1) / PPS;
     const int nk = (n_steps - wave + NW - 1) / NW;
+    // Prefetches are unconditional (rows clamped to the last attended one, an
+    // L2 hit past the wave's range), so a 16-bit cache's loads are widened
+    // where they are used, not right after a conditional load (which would
+    // wait for it on the spot).
+    const int lim = max(mem_rows, 1);
 #pragma unroll
     for (int d = 1; d < DEPTH; ++d) {
-        if (d < nk) {
-            load8(kbuf[d], kb + row_off(d));
-            load8(vbuf[d], vb + row_off(d));
-        }
+        load_raw<T>(kbuf[d], kb + row_off(d, lim), c);
+        load_raw<T>(vbuf[d], vb + row_off(d, lim), c);
+        __builtin_amdgcn_sched_barrier(0);
     }
     for (int k0 = 0; k0 < nk; k0 += DEPTH) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             const int k = k0 + d;
-            if (k >= nk) break;
-            const bool valid = (wave + NW * k) * PPS + slot < mem_rows;
+            if (k < nk) {
+                const bool valid = (wave + NW * k) * PPS + slot < mem_rows;
+                float kf[kDimsPerLane], vf[kDimsPerLane];
+                widen<T>(kf, kbuf[d]);
+                widen<T>(vf, vbuf[d]);
 #pragma unroll
-            for (int t = 0; t < kDimsPerLane; ++t) vbuf[d][t] = valid ? vbuf[d][t] : 0.f;
-            attend<1, 1, true>(q, st, kbuf[d], vbuf[d], valid);
-            if (k + DEPTH < nk) {
-                load8(kbuf[d], kb + row_off(k + DEPTH));
-                load8(vbuf[d], vb + row_off(k + DEPTH));
+                for (int t = 0; t < kDimsPerLane; ++t) vf[t] = valid ? vf[t] : 0.f;
+                attend<1, 1, true>(q, st, kf, vf, valid);
             }
+            load_raw<T>(kbuf[d], kb + row_off(k + DEPTH, lim), c);
+            load_raw<T>(vbuf[d], vb + row_off(k + DEPTH, lim), c);
         }
     }
 
@@ -611,12 +848,9 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     if (MODE == kLayer && wave == 0) {
         if (new_lane) {
             rope8(kn, cs_row, c);
-            round8(kn, kb);
-            round8(vn, kb);
-            if (head % G == 0) {
-                store8(reinterpret_cast<T*>(a.k_out) + (size_t)pos * ROW + lane_col, kn);
-                store8(reinterpret_cast<T*>(a.v_out) + (size_t)pos * ROW + lane_col, vn);
-            }
+            const bool store = head % G == 0;
+            put_row<T>(kn, reinterpret_cast<char*>(a.k_out) + (size_t)pos * ROWB + lane_col, c, store);
+            put_row<T>(vn, reinterpret_cast<char*>(a.v_out) + (size_t)pos * ROWB + lane_col, c, store);
         } else {
 #pragma unroll
             for (int t = 0; t < kDimsPerLane; ++t) kn[t] = vn[t] = 0.f;
@@ -636,7 +870,7 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
     int n_pos, pos;
     size_t base;
-    if (!seq_geometry<KV, MODE>(a, seq, n_pos, pos, base)) return;
+    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) return;
     if (n_pos <= 0) return;
     const int n_act = (n_pos + a.split_len - 1) / a.split_len;
     if (n_act <= 1 || n_act > a.n_splits) return;
@@ -700,26 +934,52 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
         combine_body<G, KV, MODE>(a);                                                              \
     }
 
-// 16-bit caches: the default group (8 waves) and head (8 waves) kernels.
-#define TMAC_MODE_KERNELS16(G, KV, M, MODE, TN, T)                                                     \
+// Narrow caches (bf16, fp16, Q8_0): the default group (8 waves) and head
+// (8 waves) kernels.
+#define TMAC_MODE_KERNELS16(G, KV, M, MODE, TN, T, DEPTH)                                              \
     extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_##M##_##TN##_g##G##_kv##KV(     \
         DecodeArgs a) {                                                                                \
-        decode_body<T, G, KV, kGroupWaves, kPrefetchDepth16, MODE, false>(a);                          \
+        decode_body<T, G, KV, kGroupWaves, DEPTH, MODE, false>(a);                                     \
     }                                                                                                  \
     extern "C" __global__ __launch_bounds__(512) void tmac_##M##_##TN##_head8_g##G##_kv##KV(DecodeArgs a) { \
         head_body<T, G, KV, 8, kHeadPrefetchDepth, MODE>(a);                                           \
     }
 
-#define TMAC_DECODE_KERNELS(G, KV)                           \
-    TMAC_MODE_KERNELS(G, KV, decode_u, kUniform)              \
-    TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)               \
-    TMAC_MODE_KERNELS(G, KV, layer, kLayer)                   \
-    TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, bf16, __bf16) \
-    TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, bf16, __bf16)  \
-    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, bf16, __bf16)      \
-    TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, f16, _Float16) \
-    TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, f16, _Float16)  \
-    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, f16, _Float16)
+// Paged caches (any element type): decode over block tables, and the batched
+// layer step.  Group kernel only (flat unit grid).
+#define TMAC_PAGED_KERNELS(G, KV, TN, T, DEPTH)                                                        \
+    extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_decode_p_##TN##_g##G##_kv##KV(  \
+        DecodeArgs a) {                                                                                \
+        decode_body<T, G, KV, kGroupWaves, DEPTH, kPaged, false>(a);                                   \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_layer_p_##TN##_g##G##_kv##KV(   \
+        DecodeArgs a) {                                                                                \
+        decode_body<T, G, KV, kGroupWaves, DEPTH, kPagedLayer, false>(a);                              \
+    }
+
+#define TMAC_DECODE_KERNELS(G, KV)                                                     \
+    TMAC_MODE_KERNELS(G, KV, decode_u, kUniform)                                        \
+    TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)                                         \
+    TMAC_MODE_KERNELS(G, KV, layer, kLayer)                                             \
+    TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, bf16, __bf16, kPrefetchDepth16)      \
+    TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, bf16, __bf16, kPrefetchDepth16)       \
+    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, bf16, __bf16, kPrefetchDepth16)           \
+    TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, f16, _Float16, kPrefetchDepth16)     \
+    TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, f16, _Float16, kPrefetchDepth16)      \
+    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, f16, _Float16, kPrefetchDepth16)          \
+    TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, q8, q8_0_t, kPrefetchDepthQ8)        \
+    TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, q8, q8_0_t, kPrefetchDepthQ8)         \
+    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, q8, q8_0_t, kPrefetchDepthQ8)             \
+    TMAC_PAGED_KERNELS(G, KV, f32, float, kPrefetchDepth)                               \
+    TMAC_PAGED_KERNELS(G, KV, bf16, __bf16, kPrefetchDepth16)                           \
+    TMAC_PAGED_KERNELS(G, KV, f16, _Float16, kPrefetchDepth16)                          \
+    TMAC_PAGED_KERNELS(G, KV, q8, q8_0_t, kPrefetchDepthQ8)                             \
+    extern "C" __global__ __launch_bounds__(64) void tmac_decode_p_combine_g##G##_kv##KV(DecodeArgs a) { \
+        combine_body<G, KV, kPaged>(a);                                                 \
+    }                                                                                   \
+    extern "C" __global__ __launch_bounds__(64) void tmac_layer_p_combine_g##G##_kv##KV(DecodeArgs a) { \
+        combine_body<G, KV, kPagedLayer>(a);                                            \
+    }
 
 // (query heads per kv head, kv heads).  Qwen2-0.5B is (7, 2).
 TMAC_DECODE_KERNELS(7, 2)
@@ -1158,10 +1418,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ unsigned ld16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 
-__device__ __forceinline__ float half_bits_to_float(unsigned h) {
-    return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
-}
-
 extern "C" __global__ __launch_bounds__(kQkvWaves * 64) void tmac_qkv(QkvArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1329,6 +1585,23 @@ extern "C" __global__ __launch_bounds__(256) void tmac_cvt16(CvtArgs a) {
         reinterpret_cast<__bf16*>(a.dst)[i] = (__bf16)a.src[i];
     else
         reinterpret_cast<_Float16*>(a.dst)[i] = (_Float16)a.src[i];
+}
+
+// Fills a Q8_0 cache from fp32 values: n / 64 head rows, each quantized as
+// the layer step quantizes a new row (put_row<q8_0_t>), one 8-lane slot per
+// head row.
+extern "C" __global__ __launch_bounds__(256) void tmac_cvt_q8(CvtArgs a) {
+    const int c = threadIdx.x & 7;
+    const int64_t hr = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const bool ok = hr < a.n / kHeadDim;  // the same for the 8 lanes of a slot
+    float x[8];
+    if (ok) {
+        load8(x, a.src + hr * kHeadDim + 4 * c);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x[t] = 0.f;
+    }
+    put_row<q8_0_t>(x, reinterpret_cast<char*>(a.dst) + hr * kQ8HeadBytes + 4 * c, c, ok);
 }
 
 // Device-side position for graph replays: *pos = value, or *pos += value.

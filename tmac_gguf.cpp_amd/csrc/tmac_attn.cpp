@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdio>
@@ -49,6 +50,7 @@ using tmac::kGroupWaves;
 using tmac::kHeadWaves;
 using tmac::kMaxSplits;
 using tmac::kSlotsPerWave;
+using tmac::kPageRows;
 
 namespace {
 
@@ -56,6 +58,10 @@ constexpr int kHeadMaxRows = 1024;  // automatic choice: head kernel up to this 
 // (G = n_head / n_kv_head, KV = n_kv_head) pairs compiled into the code object.
 constexpr int kShapes[][2] = {{7, 2}, {1, 1}, {1, 2}, {2, 2}, {4, 2}, {4, 4}, {8, 1}};
 enum { kModeUniform = 0, kModeRagged = 1, kModeLayer = 2 };
+enum { kPagedDecode = 0, kPagedLayer = 1 };
+constexpr int kNarrowTypes = 3;  // TMAC_KV_BF16, TMAC_KV_F16, TMAC_KV_Q8_0 (index kv_dtype - 1)
+const char* const kTypeName[4] = {"f32", "bf16", "f16", "q8"};  // by kv_dtype
+
 
 struct RopeTable {
     int head_dim;
@@ -95,12 +101,14 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head8[3];    // head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> head4[3];    // head kernel, 4 waves
     std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
-    std::map<std::pair<int, int>, hipFunction_t> decode16[2][3];  // 16-bit caches (bf16, fp16): group kernel
-    std::map<std::pair<int, int>, hipFunction_t> head16[2][3];    // 16-bit caches: head kernel, 8 waves
+    std::map<std::pair<int, int>, hipFunction_t> decode_n[kNarrowTypes][3];  // bf16 / fp16 / Q8_0 caches: group kernel
+    std::map<std::pair<int, int>, hipFunction_t> head_n[kNarrowTypes][3];    // the same: head kernel, 8 waves
+    std::map<std::pair<int, int>, hipFunction_t> paged[4][2];  // paged caches by kv_dtype: decode, layer step
+    std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
-                  k_kq = nullptr;
+                  k_kq = nullptr, k_cvt_q8 = nullptr;
     float* ws = nullptr;
     size_t ws_floats = 0;
     int* err = nullptr;
@@ -159,12 +167,14 @@ struct Kernels {
 };
 
 // Validates the attention shape shared by every decode entry point and picks
-// the kernels for cache element type `dt` (TMAC_KV_F32 / _BF16 / _F16; the
-// 16-bit caches use the default 8-wave group and head kernels).
+// the kernels for cache element type `dt` (TMAC_KV_F32 / _BF16 / _F16 / _Q8_0;
+// the narrow caches use the default 8-wave group and head kernels).  paged:
+// -1, or kPagedDecode / kPagedLayer for the paged kernels (group kernel only).
 int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kernels* k, int mode,
-                int dt = TMAC_KV_F32) {
-    if (dt != TMAC_KV_F32 && dt != TMAC_KV_BF16 && dt != TMAC_KV_F16)
-        return fail(ctx, TMAC_ERR_INVALID_ARG, "kv_dtype must be TMAC_KV_F32, TMAC_KV_BF16 or TMAC_KV_F16");
+                int dt = TMAC_KV_F32, int paged = -1) {
+    if (dt != TMAC_KV_F32 && dt != TMAC_KV_BF16 && dt != TMAC_KV_F16 && dt != TMAC_KV_Q8_0)
+        return fail(ctx, TMAC_ERR_INVALID_ARG,
+                    "kv_dtype must be TMAC_KV_F32, TMAC_KV_BF16, TMAC_KV_F16 or TMAC_KV_Q8_0");
     if (head_dim != kHeadDim)
         return fail(ctx, TMAC_ERR_UNSUPPORTED, "head_dim must be 64 (got " + std::to_string(head_dim) + ")");
     if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head != 0)
@@ -183,9 +193,15 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
         k->combine = ctx->combine[mode].at({g, n_kv_head});
         if (dt != TMAC_KV_F32) {
             k->group_waves = 8;
-            k->group = ctx->decode16[dt - 1][mode].at({g, n_kv_head});
+            k->group = ctx->decode_n[dt - 1][mode].at({g, n_kv_head});
             k->head_waves = 8;
-            k->head = ctx->head16[dt - 1][mode].at({g, n_kv_head});
+            k->head = ctx->head_n[dt - 1][mode].at({g, n_kv_head});
+        }
+        if (paged >= 0) {
+            k->group_waves = kGroupWaves;
+            k->group = ctx->paged[dt][paged].at({g, n_kv_head});
+            k->head = nullptr;
+            k->combine = ctx->combine_p[paged].at({g, n_kv_head});
         }
     }
     return TMAC_OK;
@@ -199,9 +215,9 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
 // With `total_rows` (ragged batches: the sum of all lengths, when the caller
 // knows it) the split length is total/target instead, so the workgroups that
 // actually have rows come close to one per CU whatever the length mix.
-void choose_split(const tmac_context* ctx, int n_seq, int n_pos, int n_kv_head, int* split_len, int* n_splits,
-                  int64_t total_rows = 0) {
-    const int round = (int)ctx->opt_group_waves * (kSlotsPerWave / n_kv_head);
+void choose_split(const tmac_context* ctx, int waves, int n_seq, int n_pos, int n_kv_head, int* split_len,
+                  int* n_splits, int64_t total_rows = 0) {
+    const int round = waves * (kSlotsPerWave / n_kv_head);
     const int rounds = (n_pos + round - 1) / round;
     int len;
     const int64_t target_groups = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : (int64_t)ctx->n_cu;
@@ -322,14 +338,15 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     a.blocked = (int)ctx->opt_blocked;
     a.err = ctx->err;
     if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
-    if (use_head_kernel(ctx, n_seq, a.n_head, grid_rows)) {
+    const bool unit_grid = a.lengths || a.positions;  // ragged and paged modes
+    if (k.head && use_head_kernel(ctx, n_seq, a.n_head, grid_rows)) {
         a.split_len = grid_rows;
         a.n_splits = 1;
         a.ws = nullptr;
         return launch(ctx, k.head, (unsigned)a.n_head, (unsigned)n_seq, k.head_waves * 64, stream, &a);
     }
     int split_len = 0, n_splits = 0;
-    choose_split(ctx, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows);
+    choose_split(ctx, k.group_waves, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows);
     a.split_len = split_len;
     a.n_splits = n_splits;
     if (n_splits > 1) {
@@ -342,7 +359,7 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     }
     a.n_seq = n_seq;
     int rc;
-    if (a.lengths) {  // ragged: flat unit grid, n_seq * n_splits bounds the unit count
+    if (unit_grid) {  // flat unit grid, n_seq * n_splits bounds the unit count
         const int64_t units = (int64_t)n_seq * n_splits;
         if (units > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: too many splits");
         rc = launch(ctx, k.group, (unsigned)units, 1, k.group_waves * 64, stream, &a);
@@ -420,16 +437,29 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->decode[m][{sh[0], sh[1]}] = f;
-            for (int dt = 0; dt < 2; dt++) {
-                const char* tn = dt == 0 ? "bf16" : "f16";
+            for (int dt = 0; dt < kNarrowTypes; dt++) {
+                const char* tn = kTypeName[dt + 1];
                 std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mode_prefix[m], tn, sh[0], sh[1]);
                 if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
-                ctx->decode16[dt][m][{sh[0], sh[1]}] = f;
+                ctx->decode_n[dt][m][{sh[0], sh[1]}] = f;
                 std::snprintf(name, sizeof(name), "%s_%s_head8_g%d_kv%d", mode_prefix[m], tn, sh[0], sh[1]);
                 if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
-                ctx->head16[dt][m][{sh[0], sh[1]}] = f;
+                ctx->head_n[dt][m][{sh[0], sh[1]}] = f;
+            }
+            if (m < 2) {  // paged kernels: m = kPagedDecode, kPagedLayer
+                const char* pp = m == kPagedDecode ? "tmac_decode_p" : "tmac_layer_p";
+                for (int dt = 0; dt < 4; dt++) {
+                    std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", pp, kTypeName[dt], sh[0], sh[1]);
+                    if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                        return bail(hip_fail(ctx, e, name));
+                    ctx->paged[dt][m][{sh[0], sh[1]}] = f;
+                }
+                std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", pp, sh[0], sh[1]);
+                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                    return bail(hip_fail(ctx, e, name));
+                ctx->combine_p[m][{sh[0], sh[1]}] = f;
             }
             std::snprintf(name, sizeof(name), "%s_g4w_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
             if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
@@ -470,7 +500,8 @@ int tmac_init(tmac_context** out, int device) {
         (e = hipModuleGetFunction(&ctx->k_pos, ctx->module, "tmac_pos_update")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->k_qkv, ctx->module, "tmac_qkv")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->k_cvt16, ctx->module, "tmac_cvt16")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_kq, ctx->module, "tmac_matmul_kq")) != hipSuccess)
+        (e = hipModuleGetFunction(&ctx->k_kq, ctx->module, "tmac_matmul_kq")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->k_cvt_q8, ctx->module, "tmac_cvt_q8")) != hipSuccess)
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
@@ -672,17 +703,109 @@ int tmac_layer_attention_devpos_kv(tmac_context* ctx, tmac_stream stream, int kv
                         head_dim, 0, pos_dev, capacity, base, kv_dtype);
 }
 
+// Shared checks of the paged entry points.
+static int check_paged(tmac_context* ctx, const char* what, const void* k_pages, const void* v_pages, int n_pages,
+                       const int32_t* block_table, int max_pages, int max_len) {
+    if (!k_pages || !v_pages || !block_table)
+        return fail(ctx, TMAC_ERR_NULL_POINTER, std::string(what) + ": null buffer");
+    if (!aligned16(k_pages) || !aligned16(v_pages) || (uintptr_t)block_table % 4)
+        return fail(ctx, TMAC_ERR_MISALIGNED, std::string(what) + ": misaligned pool or block table");
+    if (n_pages < 1 || max_pages < 1 || max_len < 1 || (int64_t)max_len > (int64_t)max_pages * kPageRows)
+        return fail(ctx, TMAC_ERR_INVALID_ARG,
+                    std::string(what) + ": need n_pages, max_pages >= 1 and 1 <= max_len <= 16 * max_pages");
+    return TMAC_OK;
+}
+
+int tmac_attention_decode_paged(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                const void* k_pages, const void* v_pages, int n_pages,
+                                const int32_t* block_table, int max_pages, const int32_t* lengths,
+                                float* out, int n_seq, int n_head, int n_kv_head, int head_dim,
+                                int max_len, int64_t total_rows) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !lengths || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "decode_paged: null buffer");
+    if (!aligned16(q) || !aligned16(out) || (uintptr_t)lengths % 4)
+        return fail(ctx, TMAC_ERR_MISALIGNED, "decode_paged: q and out must be 16-byte aligned");
+    Kernels kern;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeRagged, kv_dtype, kPagedDecode))) return rc;
+    if ((rc = check_paged(ctx, "decode_paged", k_pages, v_pages, n_pages, block_table, max_pages, max_len)))
+        return rc;
+    if (n_seq < 0 || total_rows < 0) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_paged: n_seq, total_rows >= 0");
+    if (n_seq == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    DecodeArgs a{};
+    a.q = q;
+    a.k = static_cast<const float*>(k_pages);
+    a.v = static_cast<const float*>(v_pages);
+    a.out = out;
+    a.lengths = lengths;
+    a.n_head = n_head;
+    a.block_table = block_table;
+    a.max_pages = max_pages;
+    a.n_pages = n_pages;
+    return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head, total_rows);
+}
+
+int tmac_layer_attention_paged(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                               const float* k_new, const float* v_new, void* k_pages, void* v_pages,
+                               int n_pages, const int32_t* block_table, int max_pages,
+                               const int32_t* positions, float* out, int n_seq, int n_head, int n_kv_head,
+                               int head_dim, int max_len, float base) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !k_new || !v_new || !positions || !out)
+        return fail(ctx, TMAC_ERR_NULL_POINTER, "layer_attention_paged: null buffer");
+    if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new) || !aligned16(out) || (uintptr_t)positions % 4)
+        return fail(ctx, TMAC_ERR_MISALIGNED, "layer_attention_paged: q, k_new, v_new, out must be 16-byte aligned");
+    Kernels kern;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, &kern, kModeLayer, kv_dtype, kPagedLayer))) return rc;
+    if ((rc = check_paged(ctx, "layer_attention_paged", k_pages, v_pages, n_pages, block_table, max_pages,
+                          max_len)))
+        return rc;
+    if (n_seq < 0) return fail(ctx, TMAC_ERR_INVALID_ARG, "layer_attention_paged: n_seq < 0");
+    if (!(base > 0.f) || !std::isfinite(base))
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "layer_attention_paged: bad base");
+    if (n_seq == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    const RopeTable* rt = nullptr;
+    if ((rc = rope_table(ctx, (hipStream_t)stream, head_dim, base, max_len, &rt))) return rc;
+    DecodeArgs a{};
+    a.q = q;
+    a.k = static_cast<const float*>(k_pages);
+    a.v = static_cast<const float*>(v_pages);
+    a.out = out;
+    a.n_head = n_head;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.k_out = static_cast<float*>(k_pages);
+    a.v_out = static_cast<float*>(v_pages);
+    a.rope_cs = rt->dev;
+    a.rope_rows = rt->rows;
+    a.capacity = (int)std::min<int64_t>((int64_t)max_pages * kPageRows, INT_MAX);
+    a.positions = positions;
+    a.block_table = block_table;
+    a.max_pages = max_pages;
+    a.n_pages = n_pages;
+    return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head);
+}
+
 int tmac_kv_convert(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* src, void* dst, int64_t n) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
-    if (kv_dtype != TMAC_KV_BF16 && kv_dtype != TMAC_KV_F16)
-        return fail(ctx, TMAC_ERR_INVALID_ARG, "kv_convert: kv_dtype must be TMAC_KV_BF16 or TMAC_KV_F16");
+    if (kv_dtype != TMAC_KV_BF16 && kv_dtype != TMAC_KV_F16 && kv_dtype != TMAC_KV_Q8_0)
+        return fail(ctx, TMAC_ERR_INVALID_ARG,
+                    "kv_convert: kv_dtype must be TMAC_KV_BF16, TMAC_KV_F16 or TMAC_KV_Q8_0");
     if (!src || !dst) return fail(ctx, TMAC_ERR_NULL_POINTER, "kv_convert: null buffer");
     if (n < 0 || (n + 255) / 256 > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "kv_convert: bad count");
-    if (((uintptr_t)src % 4) || ((uintptr_t)dst % 2)) return fail(ctx, TMAC_ERR_MISALIGNED, "kv_convert: misaligned");
+    const bool q8 = kv_dtype == TMAC_KV_Q8_0;
+    if (q8 && n % kHeadDim) return fail(ctx, TMAC_ERR_INVALID_ARG, "kv_convert: Q8_0 needs n % 64 == 0");
+    if (q8 ? (!aligned16(src) || (uintptr_t)dst % 4) : ((uintptr_t)src % 4 || (uintptr_t)dst % 2))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "kv_convert: misaligned");
     if (n == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
     CvtArgs a{src, dst, n, kv_dtype};
+    if (q8)  // 32 head rows of 64 values per 256-thread workgroup
+        return launch(ctx, ctx->k_cvt_q8, (unsigned)((n / kHeadDim + 31) / 32), 1, 256, (hipStream_t)stream, &a);
     return launch(ctx, ctx->k_cvt16, (unsigned)((n + 255) / 256), 1, 256, (hipStream_t)stream, &a);
 }
 
@@ -907,7 +1030,7 @@ int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_
         *n_splits = 0;  // 0 = head kernel (one workgroup per query head)
         return TMAC_OK;
     }
-    choose_split(ctx, n_seq, n_pos, n_kv_head, split_len, n_splits);
+    choose_split(ctx, (int)ctx->opt_group_waves, n_seq, n_pos, n_kv_head, split_len, n_splits);
     return TMAC_OK;
 }
 

@@ -41,6 +41,9 @@ TMAC_Q6_K = 14
 TMAC_KV_F32 = 0
 TMAC_KV_BF16 = 1
 TMAC_KV_F16 = 2
+TMAC_KV_Q8_0 = 3
+PAGE_ROWS = 16           # rows per page of a paged cache
+Q8_HEAD_BYTES = 68       # Q8_0 cache: bytes per (row, kv head): int8 q[64], fp16 d0, d1
 TMAC_OPT_SPLIT_LEN = 1
 TMAC_OPT_TARGET_GROUPS = 2
 TMAC_OPT_KERNEL = 3
@@ -77,6 +80,10 @@ SIGNATURES = {
     "tmac_layer_attention_devpos_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i,
                                             _f]),
     "tmac_kv_convert": (_i, [_vp, _vp, _i, _vp, _vp, _i64]),
+    "tmac_attention_decode_paged": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i,
+                                         _i64]),
+    "tmac_layer_attention_paged": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _i,
+                                        _i, _i, _f]),
     "tmac_matmul_q8_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "tmac_matmul_q5_0": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp]),
     "tmac_matmul_add": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
@@ -457,6 +464,27 @@ class Context:
         rc = self.lib.tmac_kv_convert(self.handle, stream, kv_dtype, _p(src), _p(dst), n)
         if check:
             self._check(rc, "kv_convert")
+        return rc
+
+    def decode_paged(self, q, k_pages, v_pages, n_pages, block_table, max_pages, lengths, out, n_seq, n_head,
+                     n_kv_head, head_dim, max_len, total_rows=0, stream=None, check=True,
+                     kv_dtype=TMAC_KV_F32) -> int:
+        rc = self.lib.tmac_attention_decode_paged(self.handle, stream, kv_dtype, _p(q), _p(k_pages), _p(v_pages),
+                                                  n_pages, _p(block_table), max_pages, _p(lengths), _p(out),
+                                                  n_seq, n_head, n_kv_head, head_dim, max_len, total_rows)
+        if check:
+            self._check(rc, "decode_paged")
+        return rc
+
+    def layer_attention_paged(self, q, k_new, v_new, k_pages, v_pages, n_pages, block_table, max_pages,
+                              positions, out, n_seq, n_head, n_kv_head, head_dim, max_len, base=1e6, stream=None,
+                              check=True, kv_dtype=TMAC_KV_F32) -> int:
+        rc = self.lib.tmac_layer_attention_paged(self.handle, stream, kv_dtype, _p(q), _p(k_new), _p(v_new),
+                                                 _p(k_pages), _p(v_pages), n_pages, _p(block_table), max_pages,
+                                                 _p(positions), _p(out), n_seq, n_head, n_kv_head, head_dim,
+                                                 max_len, base)
+        if check:
+            self._check(rc, "layer_attention_paged")
         return rc
 
     def prefill(self, q, k, v, out, n_seq, n_q, prefix_len, seq_stride, n_head, n_kv_head, head_dim,
