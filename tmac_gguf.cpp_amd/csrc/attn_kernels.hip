@@ -157,23 +157,43 @@ struct RawRow<float> {
     float w[8];
 };
 
-// p points at the lane's dim 4c of a head row.
-template <typename T>
+// A load of a cache word: non-temporal (the `nt` cache policy) when NT.
+template <bool NT, typename V>
+__device__ __forceinline__ V ld(const char* p) {
+    if constexpr (NT)
+        return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+    else
+        return *reinterpret_cast<const V*>(p);
+}
+
+// p points at the lane's dim 4c of a head row.  The group kernel reads every
+// cache row once per launch, so it streams them non-temporally (NT): at
+// config 3 that moved the fp32 decode from 185 to 170 us (72% -> 79% of HBM
+// peak), the streamed rows no longer displacing useful lines.  The head
+// kernel reads each row once per query head, through L2: temporal loads.
+template <typename T, bool NT>
 __device__ __forceinline__ void load_raw(RawRow<T>& r, const char* p, int c) {
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
     typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
     if constexpr (sizeof(T) == 4) {
-        load8(r.w, reinterpret_cast<const float*>(p));
+        const f32x4_t a = ld<NT, f32x4_t>(p);
+        const f32x4_t b = ld<NT, f32x4_t>(p + 32 * sizeof(float));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            r.w[t] = a[t];
+            r.w[4 + t] = b[t];
+        }
     } else if constexpr (sizeof(T) == 2) {
-        const u32x2 a = *reinterpret_cast<const u32x2*>(p);
-        const u32x2 b = *reinterpret_cast<const u32x2*>(p + 32 * sizeof(T));
+        const u32x2 a = ld<NT, u32x2>(p);
+        const u32x2 b = ld<NT, u32x2>(p + 32 * sizeof(T));
         r.w[0] = a[0];
         r.w[1] = a[1];
         r.w[2] = b[0];
         r.w[3] = b[1];
     } else {
-        r.w[0] = *reinterpret_cast<const unsigned*>(p);            // dims 4c..4c+3
-        r.w[1] = *reinterpret_cast<const unsigned*>(p + 32);       // dims 32+4c..32+4c+3
-        r.w[2] = *reinterpret_cast<const unsigned*>(p + 64 - 4 * c);  // d0 | d1 << 16
+        r.w[0] = ld<NT, unsigned>(p);               // dims 4c..4c+3
+        r.w[1] = ld<NT, unsigned>(p + 32);          // dims 32+4c..32+4c+3
+        r.w[2] = ld<NT, unsigned>(p + 64 - 4 * c);  // d0 | d1 << 16
     }
 }
 
@@ -204,10 +224,10 @@ __device__ __forceinline__ void widen(float (&x)[8], const RawRow<T>& r) {
     }
 }
 
-template <typename T>
+template <typename T, bool NT>
 __device__ __forceinline__ void load_row(float (&x)[8], const char* p, int c) {
     RawRow<T> r;
-    load_raw<T>(r, p, c);
+    load_raw<T, NT>(r, p, c);
     widen<T>(x, r);
 }
 
@@ -422,17 +442,17 @@ __device__ __forceinline__ void attend_rows(const char* __restrict__ kb, const c
         // assignment across iterations; a conditional load would make the
         // compiler rotate buffers with copies, which must first wait for all
         // loads in flight.
-        // Narrow caches: the prologue issues step 0 first, then step 1, ...
-        // (the scheduling barrier keeps that order).  The wait at the loop
-        // head covers both the loop entry and the back edge, so with another
-        // prologue order the entry path forces a wait for (nearly) every load
-        // in flight on every iteration (4% slower at config 3 with a bf16
-        // cache).  The fp32 kernel measured 1% faster without the barrier.
+        // The prologue issues step 0 first, then step 1, ... (the scheduling
+        // barrier keeps that order).  The wait at the loop head covers both
+        // the loop entry and the back edge, so with another prologue order
+        // the entry path forces a wait for (nearly) every load in flight on
+        // every iteration (2% slower at config 3 with an fp32 cache, 4% with
+        // a bf16 cache).
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            load_raw<T>(kbuf[d], kp + at(min(d, nk - 1)), c);
-            load_raw<T>(vbuf[d], vp + at(min(d, nk - 1)), c);
-            if constexpr (sizeof(T) < sizeof(float)) __builtin_amdgcn_sched_barrier(0);
+            load_raw<T, true>(kbuf[d], kp + at(min(d, nk - 1)), c);
+            load_raw<T, true>(vbuf[d], vp + at(min(d, nk - 1)), c);
+            __builtin_amdgcn_sched_barrier(0);
         }
         for (int k0 = 0; k0 < nk; k0 += DEPTH) {
 #pragma unroll
@@ -444,8 +464,8 @@ __device__ __forceinline__ void attend_rows(const char* __restrict__ kb, const c
                     attend<G, KVS, false>(q, st, kf, vf, true);
                 }
                 const int kn = min(k0 + d + DEPTH, nk - 1);
-                load_raw<T>(kbuf[d], kp + at(kn), c);
-                load_raw<T>(vbuf[d], vp + at(kn), c);
+                load_raw<T, true>(kbuf[d], kp + at(kn), c);
+                load_raw<T, true>(vbuf[d], vp + at(kn), c);
             }
         }
     }
@@ -459,8 +479,8 @@ __device__ __forceinline__ void attend_rows(const char* __restrict__ kb, const c
         else
             off = (size_t)r * ROWB + lane_col;
         float kf[kDimsPerLane], vf[kDimsPerLane];
-        load_row<T>(kf, kb + off, c);
-        load_row<T>(vf, vb + off, c);
+        load_row<T, true>(kf, kb + off, c);
+        load_row<T, true>(vf, vb + off, c);
         attend<G, KVS, true>(q, st, kf, vf, row < n_rows);
     }
 }
@@ -772,8 +792,8 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     RawRow<T> kbuf[DEPTH], vbuf[DEPTH];
     // (bound >= 1 except for an empty ragged sequence.)
     if (MODE != kRagged || bound > 0) {
-        load_raw<T>(kbuf[0], kb + row_off(0, bound), c);
-        load_raw<T>(vbuf[0], vb + row_off(0, bound), c);
+        load_raw<T, false>(kbuf[0], kb + row_off(0, bound), c);
+        load_raw<T, false>(vbuf[0], vb + row_off(0, bound), c);
     }
 
     // 2. the attended length
@@ -821,8 +841,8 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     const int lim = max(mem_rows, 1);
 #pragma unroll
     for (int d = 1; d < DEPTH; ++d) {
-        load_raw<T>(kbuf[d], kb + row_off(d, lim), c);
-        load_raw<T>(vbuf[d], vb + row_off(d, lim), c);
+        load_raw<T, false>(kbuf[d], kb + row_off(d, lim), c);
+        load_raw<T, false>(vbuf[d], vb + row_off(d, lim), c);
         __builtin_amdgcn_sched_barrier(0);
     }
     for (int k0 = 0; k0 < nk; k0 += DEPTH) {
@@ -838,8 +858,8 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
                 for (int t = 0; t < kDimsPerLane; ++t) vf[t] = valid ? vf[t] : 0.f;
                 attend<1, 1, true>(q, st, kf, vf, valid);
             }
-            load_raw<T>(kbuf[d], kb + row_off(k + DEPTH, lim), c);
-            load_raw<T>(vbuf[d], vb + row_off(k + DEPTH, lim), c);
+            load_raw<T, false>(kbuf[d], kb + row_off(k + DEPTH, lim), c);
+            load_raw<T, false>(vbuf[d], vb + row_off(k + DEPTH, lim), c);
         }
     }
 
