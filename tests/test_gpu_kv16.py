@@ -193,3 +193,38 @@ def test_16bit_storage_error_against_fp32_cache(ctx, dt):
     err = float(np.abs(dout.numpy() - ref32).max())
     print(f"kv dtype {dt}: max |out16 - out32| = {err:.3e}")
     assert err < (2e-2 if dt == tmac_attn.TMAC_KV_BF16 else 3e-3)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("mfma", [0, 1])
+@pytest.mark.parametrize("n_pos,split_len", [(1, 0), (15, 0), (16, 0), (17, 0), (33, 0), (1000, 0), (4096, 0),
+                                             (777, 48), (300, 16), (2049, 256)])
+def test_decode_mfma_and_valu(ctx, dt, mfma, n_pos, split_len):
+    """16-bit decode on the MFMA kernel (default) and on the VALU group kernel:
+    partial last tiles, one row, forced short splits (the combine path), and
+    rows of very different magnitudes (scores far apart: the lazy max raise)."""
+    n_seq = 3
+    rng = np.random.default_rng(n_pos + split_len)
+    q = oracle.normal(1500 + n_pos, (n_seq, NH * HD))
+    k = oracle.normal(1501 + n_pos, (n_seq, n_pos, KVD)) * np.exp2(rng.uniform(-2, 2, (n_seq, n_pos, 1)))
+    # small and large query magnitudes (the fp16 path scales q per head); scores stay within ~30 (log2
+    # units), where two fp32 evaluations still agree to the contract's 1e-4
+    q[0] *= 1e-3
+    q[2] *= 4.0
+    kb = to16(k.astype(np.float32), dt)
+    vb = to16(oracle.normal(1502 + n_pos, (n_seq, n_pos, KVD)), dt)
+    dq, dk, dv, dout = ctx.upload(q), ctx.upload(kb), ctx.upload(vb), ctx.empty((n_seq, NH * HD))
+    ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, mfma)
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_GROUP)
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, split_len)
+    try:
+        ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, kv_dtype=dt)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, 1)
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+    offs = np.arange(n_seq, dtype=np.int64) * n_pos
+    ref = oracle.attention_ragged(q, widen(kb, dt).reshape(-1, KVD), widen(vb, dt).reshape(-1, KVD), offs,
+                                  np.full(n_seq, n_pos, np.int32), NH, NKV, HD, n_threads=8)
+    assert_close(dout.numpy(), ref, f"dt={dt} mfma={mfma} n_pos={n_pos} split={split_len}")
+    assert ctx.check_device_error() == 0

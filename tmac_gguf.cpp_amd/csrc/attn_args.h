@@ -16,6 +16,7 @@ constexpr int kPrefetchDepthQ8 = 8; // the same for Q8_0 caches (136-byte rows a
 constexpr int kQ8HeadBytes = 68;    // Q8_0 cache: one (row, kv head) = int8 q[64] + fp16 d0, d1
 constexpr int kPageRows = 16;       // paged caches: rows per page
 constexpr int kPageShift = 4;       // log2(kPageRows)
+constexpr int kMWavesHost = 8;      // MFMA decode kernel: waves per workgroup
 constexpr int kHeadWaves = 16;      // "head" decode kernel (short contexts): 1024 threads
 constexpr int kHeadPrefetchDepth = 2;
 constexpr int kMaxSplits = 256;     // split-KV workgroups per sequence, at most

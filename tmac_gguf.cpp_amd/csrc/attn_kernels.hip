@@ -485,6 +485,39 @@ __device__ __forceinline__ void attend_rows(const char* __restrict__ kb, const c
     }
 }
 
+// Merges NW per-wave partial states (acc over 64 dims, base-2 max m, sum l)
+// held in LDS, one thread per (head, dim), and writes the output (single
+// split) or this split's (acc, m, l) partial.  The caller synchronizes first.
+template <int NH, int NW>
+__device__ __forceinline__ void merge_waves(const float (*s_acc)[NH][kHeadDim], const float (*s_m)[NH],
+                                            const float (*s_l)[NH], bool direct, float* __restrict__ out_heads,
+                                            float* __restrict__ ws_split) {
+    for (int idx = threadIdx.x; idx < NH * kHeadDim; idx += NW * 64) {
+        const int h = idx >> 6, d = idx & 63;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][h]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = s_m[w][h];
+            const float sc = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
+            L = fmaf(s_l[w][h], sc, L);
+            A = fmaf(s_acc[w][h][d], sc, A);
+        }
+        if (direct) {
+            out_heads[idx] = A / L;
+        } else {
+            float* p = ws_split + (size_t)h * kPartialStride;
+            p[d] = A;
+            if (d == 0) {
+                p[kHeadDim] = M;
+                p[kHeadDim + 1] = L;
+            }
+        }
+    }
+}
+
 // Merges one workgroup's NW wave states (KVS*G heads) and writes either the
 // final output (single split) or this split's (acc, m, l) partial.
 template <int G, int KVS, int NW>
@@ -522,31 +555,7 @@ __device__ __forceinline__ void finish(State<G>& st, int lane, int wave, bool di
         }
     }
     __syncthreads();
-    // 3. Merge waves: one thread per (head, dim).
-    for (int idx = threadIdx.x; idx < NH * kHeadDim; idx += NW * 64) {
-        const int h = idx >> 6, d = idx & 63;
-        float M = kNegInf;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][h]);
-        float L = 0.f, A = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float mw = s_m[w][h];
-            const float sc = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
-            L = fmaf(s_l[w][h], sc, L);
-            A = fmaf(s_acc[w][h][d], sc, A);
-        }
-        if (direct) {
-            out_heads[idx] = A / L;
-        } else {
-            float* p = ws_split + (size_t)h * kPartialStride;
-            p[d] = A;
-            if (d == 0) {
-                p[kHeadDim] = M;
-                p[kHeadDim + 1] = L;
-            }
-        }
-    }
+    merge_waves<NH, NW>(s_acc, s_m, s_l, direct, out_heads, ws_split);
 }
 
 // Rows attended by sequence `seq` (n_pos) and its first cache row (base;
@@ -1418,6 +1427,376 @@ TMAC_PREFILL_KERNEL(8, 1)
 TMAC_PREFILL_PACK_KERNEL(1)
 TMAC_PREFILL_PACK_KERNEL(2)
 TMAC_PREFILL_PACK_KERNEL(4)
+
+// ---------------------------------------------------------------------------
+// Decode on MFMA for bf16 caches (v_mfma_f32_16x16x32_bf16 for q.k,
+// v_mfma_f32_16x16x16_bf16 for p.v).  The VALU group kernel spends ~20
+// instructions per (row, query head) whatever the row's bytes, so a bf16 cache
+// would be VALU-bound there; here the products run on the matrix cores and
+// the VALU only does the softmax, four values per lane per 16-row tile.
+//
+// Same workgroups as the group kernel: grid (split, sequence) or the flat unit
+// grid, 8 waves, the same splits, combine and page addressing.  Wave w takes
+// the 16-row tiles w, w + 8, ... of its range.  Per tile (16 positions):
+//   S^T (16 keys x 16 columns) = K (16 x KV*64) . Qbd^T.  Column c < n_head is
+//     query head c; Qbd is block diagonal, so column c only meets the 64 dims
+//     of its own kv head.  The pre-scaled fp32 query is split into three
+//     bf16 parts (hi + mid + lo, 2^-27 relative), three MFMAs per 32 dims: a
+//     two-part split (2^-18) left score errors of ~2e-4 with keys 8x larger
+//     than the query, outside the fp32 contract.
+//   P^T = exp2(S^T - m), online, with the lazy rescale of the VALU kernel; P
+//     is split into bf16 hi (truncated) + lo (nearest) before the p.v MFMAs.
+//   O^T (KV*64 dims x 16 columns) += V^T . P^T over KV*4 blocks of 16 dims.
+//     The V tile is copied to LDS (rows of the cache, 16-byte chunks
+//     XOR-swizzled per row) and read back with ds_read_b64_tr_b16: in each
+//     group of 16 lanes, lane 4e + j/4 ... fetches 8 bytes and lane i receives
+//     element i % 4 of lane 4e + i / 4's 8 bytes, so lane j pointing at row
+//     4g + j/4, dims 16b + 4(j % 4) hands every lane 4 consecutive keys of one
+//     dim: the V^T operand, with no VALU transposition.
+// In the S^T / P^T / O^T accumulators lane l holds column l % 16 and rows
+// 4 (l / 16) + 0..3, so P^T feeds the p.v MFMA from the same registers.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_v;
+typedef __attribute__((address_space(3))) bf16x4_v* lds_bf16x4_ptr;
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 f16x4_v;
+typedef __attribute__((address_space(3))) f16x4_v* lds_f16x4_ptr;
+
+// The 16-bit element types of the MFMA decode: operand types, the matching
+// MFMAs and transposed LDS read, and packing of fp32 pairs (nearest even).
+//   bf16: fp32's exponent range, so q and P are split as they are.
+//   fp16: q is scaled per column by a power of two (its largest |value| to
+//   [2^14, 2^15)) and P by 2^7 before splitting, so the split parts stay in
+//   fp16's normal range; both scales are undone exactly after the MFMAs.
+template <typename T>
+struct MMath;
+template <>
+struct MMath<__bf16> {
+    typedef bf16x8 v8;
+    typedef i16x4 v4;
+    static constexpr bool kScaleQ = false;
+    static constexpr float kPScale = 1.0f;
+    __device__ static unsigned pack2(float a, float b) { return bf16_pair(a, b); }
+    __device__ static float lo(unsigned w) { return __uint_as_float(w << 16); }
+    __device__ static float hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
+    __device__ static f32x4 mfma32(v8 a, v8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+    __device__ static f32x4 mfma16(v4 a, v4 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0); }
+    __device__ static v4 read_tr(char* p) {
+        return __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_ptr)p));
+    }
+};
+template <>
+struct MMath<_Float16> {
+    typedef f16x8 v8;
+    typedef f16x4 v4;
+    static constexpr bool kScaleQ = true;
+    static constexpr float kPScale = 128.0f;
+    __device__ static unsigned pack2(float a, float b) {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        const f16x2 v = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(unsigned, v);
+    }
+    __device__ static float lo(unsigned w) { return half_bits_to_float(w & 0xffffu); }
+    __device__ static float hi(unsigned w) { return half_bits_to_float(w >> 16); }
+    __device__ static f32x4 mfma32(v8 a, v8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+    __device__ static f32x4 mfma16(v4 a, v4 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+    __device__ static v4 read_tr(char* p) {
+        return __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_f16x4_ptr)p));
+    }
+};
+
+constexpr int kMTileRows = 16;  // positions per tile
+constexpr int kMWaves = kMWavesHost;
+constexpr int kMDepth = 3;      // tiles of K and V in flight per wave
+
+template <typename T, int KV>
+struct MTile {
+    static constexpr int ROWB = KV * kHeadDim * 2;   // bytes per cache row (16-bit elements)
+    static constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
+    static constexpr int NV = kMTileRows * CPR / 64; // V chunks per lane per tile
+    static constexpr int NKB = 2 * KV;               // 32-dim blocks of the q.k contraction
+    static constexpr int NMB = 4 * KV;               // 16-dim blocks of the output
+    typename MMath<T>::v8 k[NKB];
+    u32x4 v[NV];
+};
+
+template <int KV>
+__device__ __forceinline__ int mswz(int r) {  // chunk XOR of row r in the LDS copy
+    return (2 * r) & (MTile<__bf16, KV>::CPR - 1);
+}
+
+// Loads one tile: rows `row0 + 0..15` at `base` (the tile's row 0), rows at or
+// past `valid` replaced by row valid - 1 (in bounds, masked later).
+template <typename T, int KV>
+__device__ __forceinline__ void mtile_load(MTile<T, KV>& t, const char* __restrict__ kbase,
+                                           const char* __restrict__ vbase, int valid, int lane) {
+    using Tile = MTile<T, KV>;
+    typedef typename MMath<T>::v8 v8;
+    constexpr int ROWB = Tile::ROWB, CPR = Tile::CPR;
+    const int col = lane & 15, g = lane >> 4;
+    const int kr = min(col, valid - 1);
+#pragma unroll
+    for (int b = 0; b < Tile::NKB; ++b)
+        t.k[b] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(kbase + kr * ROWB + 64 * b + 16 * g));
+#pragma unroll
+    for (int i = 0; i < Tile::NV; ++i) {
+        const int q = 64 * i + lane, r = min(q / CPR, valid - 1), c = q % CPR;
+        t.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + r * ROWB + 16 * c));
+    }
+}
+
+template <typename T, int G, int KV, int MODE>
+__device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
+    using Tile = MTile<T, KV>;
+    using M = MMath<T>;
+    constexpr int ROWB = Tile::ROWB, CPR = Tile::CPR, NKB = Tile::NKB, NMB = Tile::NMB;
+    constexpr int NH = KV * G;
+    constexpr int NW = kMWaves, D = kMDepth;
+    constexpr bool PAGED = is_paged(MODE);
+    static_assert(NH <= 16, "query heads are the 16 MFMA columns");
+    static_assert(!is_layer(MODE), "the layer step runs on the VALU kernels");
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, g = lane >> 4;
+    int split = blockIdx.x, seq = blockIdx.y;
+    if (MODE == kRagged || PAGED) {
+        if (!ragged_unit(a.lengths, 0, a.n_seq, a.split_len, a.n_splits, blockIdx.x, seq, split)) return;
+    }
+    int n_pos, pos;
+    size_t base;
+    seq_geometry<MODE>(a, seq, n_pos, pos, base);
+    n_pos = __builtin_amdgcn_readfirstlane(n_pos);
+    float* out_heads = a.out + (size_t)seq * NH * kHeadDim;
+    if (n_pos <= 0) {
+        if (split == 0)
+            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_heads[i] = 0.f;
+        return;
+    }
+    const int n_act = (n_pos + a.split_len - 1) / a.split_len;
+    if (n_act > a.n_splits) {
+        if (split == 0) {
+            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_heads[i] = __builtin_nanf("");
+            if (threadIdx.x == 0) atomicOr(a.err, 2);
+        }
+        return;
+    }
+    if (split >= n_act) return;
+    const int r0 = split * a.split_len;
+    const int n_rows = min(r0 + a.split_len, n_pos) - r0;
+
+    // Q^T operands: column col, dims 32 (b % 2) + 8 g + 0..7 of kv head b / 2,
+    // zero unless head col belongs to that kv head.  Three 16-bit parts (hi +
+    // mid + lo), each rounded to nearest from the exact remainder of the
+    // previous ones.  fp16: the column is first scaled by 2^qe (exact).
+    float qx[NKB][8];
+#pragma unroll
+    for (int b = 0; b < NKB; ++b) {
+        const bool mine = col < NH && col / G == b / 2;
+        const float* qp = a.q + ((size_t)seq * NH + min(col, NH - 1)) * kHeadDim + 32 * (b % 2) + 8 * g;
+        const float4 x0 = *reinterpret_cast<const float4*>(qp);
+        const float4 x1 = *reinterpret_cast<const float4*>(qp + 4);
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) qx[b][t] = mine ? x[t] * a.qscale : 0.f;
+    }
+    float s_unscale = 1.0f;  // S^T column scale to undo (fp16)
+    if (M::kScaleQ) {
+        float mx = 0.f;
+#pragma unroll
+        for (int b = 0; b < NKB; ++b)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(qx[b][t]));
+        mx = max4_rows(mx);
+        int qe = 0;
+        if (mx > 0.f) qe = 14 - (int)((__float_as_uint(mx) >> 23) & 0xFF) + 127;  // mx * 2^qe in [2^14, 2^15)
+        qe = max(min(qe, 126), -126);
+#pragma unroll
+        for (int b = 0; b < NKB; ++b)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) qx[b][t] = __builtin_ldexpf(qx[b][t], qe);
+        s_unscale = __builtin_ldexpf(1.0f, -qe);
+    }
+    typename M::v8 qpart[3][NKB];
+#pragma unroll
+    for (int b = 0; b < NKB; ++b) {
+        u32x4 w[3];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float e0 = qx[b][2 * t], e1 = qx[b][2 * t + 1];
+#pragma unroll
+            for (int part = 0; part < 3; ++part) {
+                w[part][t] = M::pack2(e0, e1);
+                e0 -= M::lo(w[part][t]);  // exact
+                e1 -= M::hi(w[part][t]);
+            }
+        }
+#pragma unroll
+        for (int part = 0; part < 3; ++part) qpart[part][b] = __builtin_bit_cast(typename M::v8, w[part]);
+    }
+
+    // This wave's LDS copy of the current V tile, and its lane offsets.
+    __shared__ __attribute__((aligned(16))) char s_v[NW][kMTileRows * ROWB];
+    char* sv = s_v[wave];
+    int wr_off[Tile::NV];
+#pragma unroll
+    for (int i = 0; i < Tile::NV; ++i) {
+        const int q = 64 * i + lane, r = q / CPR, c = q % CPR;
+        wr_off[i] = r * ROWB + 16 * (c ^ mswz<KV>(r));
+    }
+    int rd_off[NMB];
+    {
+        const int j = col, r = 4 * g + j / 4;
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+            rd_off[mb] = r * ROWB + 16 * ((2 * mb + (j & 3) / 2) ^ mswz<KV>(r)) + 8 * (j & 1);
+    }
+
+    f32x4 acc[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = kNegInf, l = 0.f;
+
+    const char* kc = reinterpret_cast<const char*>(a.k) + (PAGED ? 0 : base * ROWB);
+    const char* vc = reinterpret_cast<const char*>(a.v) + (PAGED ? 0 : base * ROWB);
+    const PageMap pm{PAGED ? a.block_table + (size_t)seq * a.max_pages : nullptr, r0, a.n_pages};
+    unsigned bad = 0;
+    auto tile_off = [&](int t) -> size_t {  // byte offset of tile t's row 0 from kc / vc
+        const int row = r0 + t * kMTileRows;
+        if (!PAGED) return (size_t)row * ROWB;
+        return (size_t)page_of(pm, row, bad) * kPageRows * ROWB;
+    };
+
+    // One tile: q.k, online softmax, p.v.  `valid` rows of the tile are real.
+    auto compute = [&](const Tile& t, int valid) {
+#pragma unroll
+        for (int i = 0; i < Tile::NV; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t.v[i];
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < NKB; ++b)
+#pragma unroll
+            for (int part = 2; part >= 0; --part)  // smallest part first
+                s = M::mfma32(t.k[b], qpart[part][b], s);
+        if (M::kScaleQ) s *= s_unscale;
+        if (valid < kMTileRows) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * g + i >= valid) s[i] = kNegInf;
+        }
+        float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        tm = max4_rows(tm);
+        if (__any(tm - m > kTau)) {  // raise the running max (rare after the first tile)
+            const float mn = fmaxf(m, tm);
+            const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
+            l *= alpha;
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) acc[mb] *= alpha;
+            m = mn;
+        }
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = fast_exp2(s[i] - m);  // 0 for masked keys
+            l += p[i];
+        }
+        u32x2 ph, pl;  // P^T (times kPScale) as 16-bit hi + lo
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float p0 = p[2 * i] * M::kPScale, p1 = p[2 * i + 1] * M::kPScale;
+            ph[i] = M::pack2(p0, p1);
+            pl[i] = M::pack2(p0 - M::lo(ph[i]), p1 - M::hi(ph[i]));
+        }
+        const typename M::v4 bh = __builtin_bit_cast(typename M::v4, ph);
+        const typename M::v4 bl = __builtin_bit_cast(typename M::v4, pl);
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) {
+            const typename M::v4 va = M::read_tr(sv + rd_off[mb]);
+            acc[mb] = M::mfma16(va, bh, acc[mb]);
+            acc[mb] = M::mfma16(va, bl, acc[mb]);
+        }
+    };
+
+    const int full = n_rows / kMTileRows;
+    const int nk = (full - wave + NW - 1) / NW;  // this wave's full tiles: wave + NW * k
+    if (nk > 0) {
+        Tile buf[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const size_t off = tile_off(wave + NW * min(d, nk - 1));
+            mtile_load<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int k0 = 0; k0 < nk; k0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                if (k0 + d < nk) compute(buf[d], kMTileRows);
+                const size_t off = tile_off(wave + NW * min(k0 + d + D, nk - 1));
+                mtile_load<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+            }
+        }
+    }
+    const int tail = n_rows - full * kMTileRows;
+    if (tail > 0 && (full % NW) == wave) {
+        Tile t;
+        const size_t off = tile_off(full);
+        mtile_load<T, KV>(t, kc + off, vc + off, tail, lane);
+        compute(t, tail);
+    }
+    if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
+
+    // Wave states -> LDS -> merge.  Column col's row sum is spread over the 4
+    // lane groups; its output dims 16 mm + 4 g + i live in the M-blocks of its
+    // own kv head.
+    l = sum4_rows(l);
+    if (M::kPScale != 1.0f) {  // O^T accumulated P * kPScale (a power of two)
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) acc[mb] *= 1.0f / M::kPScale;
+    }
+    __shared__ float s_acc[NW][NH][kHeadDim];
+    __shared__ float s_m[NW][NH];
+    __shared__ float s_l[NW][NH];
+    if (col < NH) {
+        const int kv = col / G;
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) {
+                if (mb == 4 * kv + mm) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s_acc[wave][col][16 * mm + 4 * g + i] = acc[mb][i];
+                }
+            }
+        }
+        if (g == 0) {
+            s_m[wave][col] = m;
+            s_l[wave][col] = l;
+        }
+    }
+    __syncthreads();
+    const bool direct = (n_act == 1);
+    float* ws_split = direct ? nullptr : a.ws + ((size_t)seq * a.n_splits + split) * NH * kPartialStride;
+    merge_waves<NH, NW>(s_acc, s_m, s_l, direct, out_heads, ws_split);
+}
+
+#define TMAC_MDECODE_KERNELS_T(G, KV, TN, T)                                                          \
+    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_u_##TN##_g##G##_kv##KV(     \
+        DecodeArgs a) {                                                                                \
+        mdecode_body<T, G, KV, kUniform>(a);                                                           \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_r_##TN##_g##G##_kv##KV(     \
+        DecodeArgs a) {                                                                                \
+        mdecode_body<T, G, KV, kRagged>(a);                                                            \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_p_##TN##_g##G##_kv##KV(     \
+        DecodeArgs a) {                                                                                \
+        mdecode_body<T, G, KV, kPaged>(a);                                                             \
+    }
+#define TMAC_MDECODE_KERNELS(G, KV)               \
+    TMAC_MDECODE_KERNELS_T(G, KV, bf16, __bf16)    \
+    TMAC_MDECODE_KERNELS_T(G, KV, f16, _Float16)
+
+TMAC_MDECODE_KERNELS(7, 2)
 
 // ---------------------------------------------------------------------------
 // QKV projection: the producer of q / k_new / v_new (fused_qkv_op,

@@ -105,6 +105,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head_n[kNarrowTypes][3];    // the same: head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> paged[4][2];  // paged caches by kv_dtype: decode, layer step
     std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
+    std::map<std::pair<int, int>, hipFunction_t> mdecode[2][3];  // MFMA decode (bf16, fp16): uniform, ragged, paged
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
@@ -120,6 +121,7 @@ struct tmac_context {
     int64_t opt_head_waves = 8;
     int64_t opt_blocked = 0;
     int64_t opt_group_waves = 8;
+    int64_t opt_mfma = 1;
     std::string last_error;
     char device_name[256] = {0};
 };
@@ -202,6 +204,16 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
             k->group = ctx->paged[dt][paged].at({g, n_kv_head});
             k->head = nullptr;
             k->combine = ctx->combine_p[paged].at({g, n_kv_head});
+        }
+        // bf16 / fp16 decode (not the layer step) on the MFMA kernel where one is built for the shape.
+        const int mm = paged == kPagedDecode ? 2 : paged < 0 && mode != kModeLayer ? mode : -1;
+        if ((dt == TMAC_KV_BF16 || dt == TMAC_KV_F16) && ctx->opt_mfma && mm >= 0) {
+            auto& tab = ctx->mdecode[dt - 1][mm];
+            auto f = tab.find({g, n_kv_head});
+            if (f != tab.end()) {
+                k->group = f->second;
+                k->group_waves = tmac::kMWavesHost;
+            }
         }
     }
     return TMAC_OK;
@@ -447,6 +459,12 @@ int tmac_init(tmac_context** out, int device) {
                 if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
                 ctx->head_n[dt][m][{sh[0], sh[1]}] = f;
+            }
+            for (int dt = 0; dt < 2; dt++) {  // MFMA decode (bf16, fp16): built for some shapes only
+                const char* mp[3] = {"tmac_mdecode_u", "tmac_mdecode_r", "tmac_mdecode_p"};
+                std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mp[m], kTypeName[dt + 1], sh[0], sh[1]);
+                if (hipModuleGetFunction(&f, ctx->module, name) == hipSuccess) ctx->mdecode[dt][m][{sh[0], sh[1]}] = f;
+                (void)hipGetLastError();
             }
             if (m < 2) {  // paged kernels: m = kPagedDecode, kPagedLayer
                 const char* pp = m == kPagedDecode ? "tmac_decode_p" : "tmac_layer_p";
@@ -1013,6 +1031,10 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
         case TMAC_OPT_KERNEL:
             if (value > TMAC_KERNEL_HEAD) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: bad kernel choice");
             ctx->opt_kernel = value;
+            return TMAC_OK;
+        case TMAC_OPT_MFMA_DECODE:
+            if (value > 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: MFMA decode is 0 or 1");
+            ctx->opt_mfma = value;
             return TMAC_OK;
         default: return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: unknown option");
     }
