@@ -228,3 +228,30 @@ def test_decode_mfma_and_valu(ctx, dt, mfma, n_pos, split_len):
                                   np.full(n_seq, n_pos, np.int32), NH, NKV, HD, n_threads=8)
     assert_close(dout.numpy(), ref, f"dt={dt} mfma={mfma} n_pos={n_pos} split={split_len}")
     assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("g,kv", [(1, 1), (1, 2), (2, 2), (4, 2), (4, 4), (8, 1)])
+def test_decode_mfma_shapes(ctx, dt, g, kv):
+    """The MFMA decode at every compiled (query heads per kv head, kv heads)
+    shape, batched and ragged, against the oracle on the widened cache."""
+    nh, kvd = g * kv, kv * HD
+    lens = np.array([700, 1, 33, 2000], np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
+    rows = int(lens.sum())
+    q = oracle.normal(1600 + 10 * g + kv, (lens.size, nh * HD))
+    kb = to16(oracle.normal(1601 + 10 * g + kv, (rows, kvd)), dt)
+    vb = to16(oracle.normal(1602 + 10 * g + kv, (rows, kvd)), dt)
+    dq, dk, dv = ctx.upload(q), ctx.upload(kb), ctx.upload(vb)
+    doffs, dlens, dout = ctx.upload(offs), ctx.upload(lens), ctx.empty((lens.size, nh * HD))
+    ctx.decode_ragged(dq, dk, dv, doffs, dlens, dout, lens.size, nh, kv, HD, int(lens.max()), kv_dtype=dt)
+    kw = widen(kb, dt).reshape(-1, kvd)
+    vw = widen(vb, dt).reshape(-1, kvd)
+    ref = oracle.attention_ragged(q, kw, vw, offs, lens, nh, kv, HD, n_threads=8)
+    assert_close(dout.numpy(), ref, f"ragged dt={dt} g={g} kv={kv}")
+    n_pos = 1000  # batched: the first 2 * 1000 rows as two sequences
+    ctx.decode_batched(dq, dk, dv, dout, 2, nh, kv, HD, n_pos, n_pos, kv_dtype=dt)
+    ref = oracle.attention_ragged(q[:2], kw, vw, np.array([0, n_pos], np.int64), np.full(2, n_pos, np.int32), nh,
+                                  kv, HD, n_threads=8)
+    assert_close(dout.numpy()[:2], ref, f"batched dt={dt} g={g} kv={kv}")
+    assert ctx.check_device_error() == 0

@@ -33,6 +33,15 @@
 
 #include "attn_args.h"
 
+// The kernels are instantiated in four parts, each built into its own code
+// object (in parallel): 0 the fp32 decode family, 1 the bf16 / fp16 / Q8_0
+// VALU decode family, 2 the paged family, 3 the MFMA decode, prefill,
+// projection and small kernels.  Without TMAC_PART every kernel is built.
+#ifndef TMAC_PART
+#define TMAC_PART -1
+#endif
+#define TMAC_IN_PART(p) (TMAC_PART < 0 || TMAC_PART == (p))
+
 using namespace tmac;
 
 namespace {
@@ -986,10 +995,16 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
         decode_body<T, G, KV, kGroupWaves, DEPTH, kPagedLayer, false>(a);                              \
     }
 
-#define TMAC_DECODE_KERNELS(G, KV)                                                     \
-    TMAC_MODE_KERNELS(G, KV, decode_u, kUniform)                                        \
-    TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)                                         \
-    TMAC_MODE_KERNELS(G, KV, layer, kLayer)                                             \
+#if TMAC_IN_PART(0)
+#define TMAC_DECODE_F32(G, KV)                       \
+    TMAC_MODE_KERNELS(G, KV, decode_u, kUniform)      \
+    TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)       \
+    TMAC_MODE_KERNELS(G, KV, layer, kLayer)
+#else
+#define TMAC_DECODE_F32(G, KV)
+#endif
+#if TMAC_IN_PART(1)
+#define TMAC_DECODE_NARROW(G, KV)                                                      \
     TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, bf16, __bf16, kPrefetchDepth16)      \
     TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, bf16, __bf16, kPrefetchDepth16)       \
     TMAC_MODE_KERNELS16(G, KV, layer, kLayer, bf16, __bf16, kPrefetchDepth16)           \
@@ -998,7 +1013,12 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     TMAC_MODE_KERNELS16(G, KV, layer, kLayer, f16, _Float16, kPrefetchDepth16)          \
     TMAC_MODE_KERNELS16(G, KV, decode_u, kUniform, q8, q8_0_t, kPrefetchDepthQ8)        \
     TMAC_MODE_KERNELS16(G, KV, decode_r, kRagged, q8, q8_0_t, kPrefetchDepthQ8)         \
-    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, q8, q8_0_t, kPrefetchDepthQ8)             \
+    TMAC_MODE_KERNELS16(G, KV, layer, kLayer, q8, q8_0_t, kPrefetchDepthQ8)
+#else
+#define TMAC_DECODE_NARROW(G, KV)
+#endif
+#if TMAC_IN_PART(2)
+#define TMAC_DECODE_PAGED(G, KV)                                                       \
     TMAC_PAGED_KERNELS(G, KV, f32, float, kPrefetchDepth)                               \
     TMAC_PAGED_KERNELS(G, KV, bf16, __bf16, kPrefetchDepth16)                           \
     TMAC_PAGED_KERNELS(G, KV, f16, _Float16, kPrefetchDepth16)                          \
@@ -1009,6 +1029,10 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     extern "C" __global__ __launch_bounds__(64) void tmac_layer_p_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, kPagedLayer>(a);                                            \
     }
+#else
+#define TMAC_DECODE_PAGED(G, KV)
+#endif
+#define TMAC_DECODE_KERNELS(G, KV) TMAC_DECODE_F32(G, KV) TMAC_DECODE_NARROW(G, KV) TMAC_DECODE_PAGED(G, KV)
 
 // (query heads per kv head, kv heads).  Qwen2-0.5B is (7, 2).
 TMAC_DECODE_KERNELS(7, 2)
@@ -1412,6 +1436,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
         PrefillArgs a) {                                                                              \
         prefill_body<G, KV>(a);                                                                       \
     }
+#if TMAC_IN_PART(3)
 TMAC_PREFILL_KERNEL(7, 2)
 TMAC_PREFILL_KERNEL(1, 1)
 TMAC_PREFILL_KERNEL(1, 2)
@@ -1427,6 +1452,7 @@ TMAC_PREFILL_KERNEL(8, 1)
 TMAC_PREFILL_PACK_KERNEL(1)
 TMAC_PREFILL_PACK_KERNEL(2)
 TMAC_PREFILL_PACK_KERNEL(4)
+#endif
 
 // ---------------------------------------------------------------------------
 // Decode on MFMA for bf16 caches (v_mfma_f32_16x16x32_bf16 for q.k,
@@ -1796,8 +1822,17 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     TMAC_MDECODE_KERNELS_T(G, KV, bf16, __bf16)    \
     TMAC_MDECODE_KERNELS_T(G, KV, f16, _Float16)
 
+#if TMAC_IN_PART(3)
 TMAC_MDECODE_KERNELS(7, 2)
+TMAC_MDECODE_KERNELS(1, 1)
+TMAC_MDECODE_KERNELS(1, 2)
+TMAC_MDECODE_KERNELS(2, 2)
+TMAC_MDECODE_KERNELS(4, 2)
+TMAC_MDECODE_KERNELS(4, 4)
+TMAC_MDECODE_KERNELS(8, 1)
+#endif
 
+#if TMAC_IN_PART(3)  // projection, RoPE, copy, conversion and position kernels
 // ---------------------------------------------------------------------------
 // QKV projection: the producer of q / k_new / v_new (fused_qkv_op,
 // metal_backend.hpp:456-489; CPU form tmac_gguf.cpp:1046-1081, dequantisation
@@ -2007,3 +2042,5 @@ extern "C" __global__ __launch_bounds__(256) void tmac_cvt_q8(CvtArgs a) {
 extern "C" __global__ __launch_bounds__(64) void tmac_pos_update(PosArgs a) {
     if (threadIdx.x == 0) *a.pos = a.add ? *a.pos + a.value : a.value;
 }
+
+#endif  // TMAC_IN_PART(3)

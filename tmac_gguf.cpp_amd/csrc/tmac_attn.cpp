@@ -27,8 +27,10 @@
 
 #include "attn_args.h"
 
-extern "C" const unsigned char tmac_attn_code_object[];
-extern "C" const uint64_t tmac_attn_code_object_size;
+// The gfx950 code objects, one per kernel part (code_object.S).
+constexpr int kCodeParts = 4;
+extern "C" const unsigned char* const tmac_attn_code_objects[kCodeParts];
+extern "C" const uint64_t tmac_attn_code_object_sizes[kCodeParts];
 
 using tmac::CopyArgs;
 using tmac::CvtArgs;
@@ -94,7 +96,7 @@ struct tmac_model {
 struct tmac_context {
     int device = -1;
     int n_cu = 0;
-    hipModule_t module = nullptr;
+    hipModule_t modules[kCodeParts] = {};
     std::map<std::pair<int, int>, hipFunction_t> decode[3];   // group kernel, by mode, (G, KV)
     std::map<std::pair<int, int>, hipFunction_t> decode4[3];  // group kernel with 4-wave workgroups
     std::map<std::pair<int, int>, hipFunction_t> head[3];     // head kernel (16 waves), same keys
@@ -147,13 +149,21 @@ int hip_fail(tmac_context* ctx, hipError_t e, const char* what) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_ctx(tmac_context* ctx) {
-    if (!ctx || !ctx->module) return TMAC_ERR_NOT_INITIALIZED;
+    if (!ctx || !ctx->modules[0]) return TMAC_ERR_NOT_INITIALIZED;
     return TMAC_OK;
 }
 
 int set_device(tmac_context* ctx) {
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     return TMAC_OK;
+}
+
+// Looks a kernel up in whichever code object part holds it.
+hipError_t get_function(tmac_context* ctx, hipFunction_t* f, const char* name) {
+    for (auto m : ctx->modules)
+        if (m && hipModuleGetFunction(f, m, name) == hipSuccess) return hipSuccess;
+    (void)hipGetLastError();
+    return hipErrorNotFound;
 }
 
 bool capturing(hipStream_t s) {
@@ -423,7 +433,8 @@ int tmac_init(tmac_context** out, int device) {
         return rc;
     }
     auto bail = [&](int rc) {
-        if (ctx->module) (void)hipModuleUnload(ctx->module);
+        for (auto& m : ctx->modules)
+            if (m) (void)hipModuleUnload(m);
         delete ctx;
         return rc;
     };
@@ -438,88 +449,89 @@ int tmac_init(tmac_context** out, int device) {
                 prop.gcnArchName);
         return bail(TMAC_ERR_UNSUPPORTED);
     }
-    if ((e = hipModuleLoadData(&ctx->module, tmac_attn_code_object)) != hipSuccess)
-        return bail(hip_fail(ctx, e, "hipModuleLoadData"));
+    for (int i = 0; i < kCodeParts; i++)
+        if ((e = hipModuleLoadData(&ctx->modules[i], tmac_attn_code_objects[i])) != hipSuccess)
+            return bail(hip_fail(ctx, e, "hipModuleLoadData"));
     const char* mode_prefix[3] = {"tmac_decode_u", "tmac_decode_r", "tmac_layer"};
     for (int m = 0; m < 3; m++) {
         for (auto& sh : kShapes) {
             char name[64];
             std::snprintf(name, sizeof(name), "%s_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
             hipFunction_t f = nullptr;
-            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+            if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->decode[m][{sh[0], sh[1]}] = f;
             for (int dt = 0; dt < kNarrowTypes; dt++) {
                 const char* tn = kTypeName[dt + 1];
                 std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mode_prefix[m], tn, sh[0], sh[1]);
-                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                if ((e = get_function(ctx, &f, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
                 ctx->decode_n[dt][m][{sh[0], sh[1]}] = f;
                 std::snprintf(name, sizeof(name), "%s_%s_head8_g%d_kv%d", mode_prefix[m], tn, sh[0], sh[1]);
-                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                if ((e = get_function(ctx, &f, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
                 ctx->head_n[dt][m][{sh[0], sh[1]}] = f;
             }
             for (int dt = 0; dt < 2; dt++) {  // MFMA decode (bf16, fp16): built for some shapes only
                 const char* mp[3] = {"tmac_mdecode_u", "tmac_mdecode_r", "tmac_mdecode_p"};
                 std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mp[m], kTypeName[dt + 1], sh[0], sh[1]);
-                if (hipModuleGetFunction(&f, ctx->module, name) == hipSuccess) ctx->mdecode[dt][m][{sh[0], sh[1]}] = f;
+                if (get_function(ctx, &f, name) == hipSuccess) ctx->mdecode[dt][m][{sh[0], sh[1]}] = f;
                 (void)hipGetLastError();
             }
             if (m < 2) {  // paged kernels: m = kPagedDecode, kPagedLayer
                 const char* pp = m == kPagedDecode ? "tmac_decode_p" : "tmac_layer_p";
                 for (int dt = 0; dt < 4; dt++) {
                     std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", pp, kTypeName[dt], sh[0], sh[1]);
-                    if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                    if ((e = get_function(ctx, &f, name)) != hipSuccess)
                         return bail(hip_fail(ctx, e, name));
                     ctx->paged[dt][m][{sh[0], sh[1]}] = f;
                 }
                 std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", pp, sh[0], sh[1]);
-                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                if ((e = get_function(ctx, &f, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
                 ctx->combine_p[m][{sh[0], sh[1]}] = f;
             }
             std::snprintf(name, sizeof(name), "%s_g4w_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
-            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+            if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->decode4[m][{sh[0], sh[1]}] = f;
             std::snprintf(name, sizeof(name), "%s_head_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
-            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+            if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->head[m][{sh[0], sh[1]}] = f;
             std::snprintf(name, sizeof(name), "%s_head8_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
-            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+            if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->head8[m][{sh[0], sh[1]}] = f;
             std::snprintf(name, sizeof(name), "%s_head4_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
-            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+            if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->head4[m][{sh[0], sh[1]}] = f;
             std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
-            if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+            if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->combine[m][{sh[0], sh[1]}] = f;
             if (m == 0) {
                 std::snprintf(name, sizeof(name), "tmac_prefill_g%d_kv%d", sh[0], sh[1]);
-                if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                if ((e = get_function(ctx, &f, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
                 ctx->prefill[{sh[0], sh[1]}] = f;
                 if (!ctx->prefill_pack.count(sh[1])) {
                     std::snprintf(name, sizeof(name), "tmac_prefill_pack_kv%d", sh[1]);
-                    if ((e = hipModuleGetFunction(&f, ctx->module, name)) != hipSuccess)
+                    if ((e = get_function(ctx, &f, name)) != hipSuccess)
                         return bail(hip_fail(ctx, e, name));
                     ctx->prefill_pack[sh[1]] = f;
                 }
             }
         }
     }
-    if ((e = hipModuleGetFunction(&ctx->k_rope, ctx->module, "tmac_rope")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_copy, ctx->module, "tmac_copy")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_pos, ctx->module, "tmac_pos_update")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_qkv, ctx->module, "tmac_qkv")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_cvt16, ctx->module, "tmac_cvt16")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_kq, ctx->module, "tmac_matmul_kq")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->k_cvt_q8, ctx->module, "tmac_cvt_q8")) != hipSuccess)
+    if ((e = get_function(ctx, &ctx->k_rope, "tmac_rope")) != hipSuccess ||
+        (e = get_function(ctx, &ctx->k_copy, "tmac_copy")) != hipSuccess ||
+        (e = get_function(ctx, &ctx->k_pos, "tmac_pos_update")) != hipSuccess ||
+        (e = get_function(ctx, &ctx->k_qkv, "tmac_qkv")) != hipSuccess ||
+        (e = get_function(ctx, &ctx->k_cvt16, "tmac_cvt16")) != hipSuccess ||
+        (e = get_function(ctx, &ctx->k_kq, "tmac_matmul_kq")) != hipSuccess ||
+        (e = get_function(ctx, &ctx->k_cvt_q8, "tmac_cvt_q8")) != hipSuccess)
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
@@ -531,13 +543,14 @@ int tmac_init(tmac_context** out, int device) {
 
 int tmac_shutdown(tmac_context* ctx) {
     if (!ctx) return TMAC_ERR_NOT_INITIALIZED;
-    if (ctx->module) {
+    if (ctx->modules[0]) {
         (void)hipSetDevice(ctx->device);
         (void)hipDeviceSynchronize();
         for (auto& t : ctx->rope) (void)hipFree(t.dev);
         if (ctx->ws) (void)hipFree(ctx->ws);
         if (ctx->err) (void)hipFree(ctx->err);
-        (void)hipModuleUnload(ctx->module);
+        for (auto& m : ctx->modules)
+            if (m) (void)hipModuleUnload(m);
     }
     delete ctx;
     return TMAC_OK;
