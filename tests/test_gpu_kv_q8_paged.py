@@ -80,23 +80,26 @@ def test_kv_convert_q8_rejects(ctx):
     assert ctx.kv_convert(Q8, d.at(1), d, 64, check=False) == tmac_attn.TMAC_ERR_MISALIGNED
 
 
+@pytest.mark.parametrize("mfma", [0, 1])
 @pytest.mark.parametrize("n_seq,n_pos,kernel", [(3, 300, tmac_attn.TMAC_KERNEL_AUTO), (2, 2000, 0), (8, 4096, 0),
                                                 (1, 700, tmac_attn.TMAC_KERNEL_HEAD),
-                                                (2, 77, tmac_attn.TMAC_KERNEL_GROUP)])
-def test_decode_batched_q8(ctx, n_seq, n_pos, kernel):
+                                                (2, 77, tmac_attn.TMAC_KERNEL_GROUP), (3, 17, 0), (2, 1, 0)])
+def test_decode_batched_q8(ctx, mfma, n_seq, n_pos, kernel):
     q = data(800 + n_pos, (n_seq, NH * HD))
     kb = store(data(801 + n_pos, (n_seq * n_pos, KVD), 2), Q8)
     vb = store(data(802 + n_pos, (n_seq * n_pos, KVD), 2), Q8)
     dq, dk, dv, dout = ctx.upload(q), ctx.upload(kb), ctx.upload(vb), ctx.empty((n_seq, NH * HD))
     ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, kernel)
+    ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, mfma)
     try:
         ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, kv_dtype=Q8)
     finally:
         ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, 1)
     offs = np.arange(n_seq, dtype=np.int64) * n_pos
     lens = np.full(n_seq, n_pos, np.int32)
     ref = oracle.attention_ragged(q, widen(kb, Q8), widen(vb, Q8), offs, lens, NH, NKV, HD, n_threads=8)
-    assert_close(dout.numpy(), ref, f"batched q8 {n_seq}x{n_pos}")
+    assert_close(dout.numpy(), ref, f"batched q8 {n_seq}x{n_pos} mfma={mfma}")
 
 
 def test_decode_ragged_q8(ctx):
@@ -426,3 +429,24 @@ def test_layer_paged_position_errors(ctx):
     kref, vref = np.zeros((6, KVD), np.float32), np.zeros((6, KVD), np.float32)
     kref[5], vref[5] = kr, vn[0]
     assert_close(got[0], oracle.attention(qr, kref, vref, NH, NKV, HD, 5), "valid sequence")
+
+
+@pytest.mark.parametrize("g,kv", [(1, 1), (2, 2), (4, 4), (8, 1)])
+def test_decode_q8_mfma_shapes(ctx, g, kv):
+    """Q8_0 decode (MFMA kernel) at other GQA shapes, ragged, with widely
+    varying row magnitudes (per-block scales from 2^-4 to 2^4)."""
+    nh, kvd = g * kv, kv * HD
+    lens = np.array([513, 1, 40, 1500], np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
+    rows = int(lens.sum())
+    q = data(1900 + g + kv, (lens.size, nh * HD))
+    kb = oracle.q8_kv_rows(data(1901 + g + kv, (rows, kvd), 4)).reshape(rows, -1)
+    vb = oracle.q8_kv_rows(data(1902 + g + kv, (rows, kvd), 4)).reshape(rows, -1)
+    dq, dk, dv = ctx.upload(q), ctx.upload(kb), ctx.upload(vb)
+    doffs, dlens, dout = ctx.upload(offs), ctx.upload(lens), ctx.empty((lens.size, nh * HD))
+    ctx.decode_ragged(dq, dk, dv, doffs, dlens, dout, lens.size, nh, kv, HD, int(lens.max()), kv_dtype=Q8)
+    kw = oracle.q8_kv_widen(kb).reshape(rows, kvd)
+    vw = oracle.q8_kv_widen(vb).reshape(rows, kvd)
+    ref = oracle.attention_ragged(q, kw, vw, offs, lens, nh, kv, HD, n_threads=8)
+    assert_close(dout.numpy(), ref, f"q8 ragged g={g} kv={kv}")
+    assert ctx.check_device_error() == 0

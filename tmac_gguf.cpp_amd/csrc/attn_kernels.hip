@@ -1573,11 +1573,86 @@ __device__ __forceinline__ void mtile_load(MTile<T, KV>& t, const char* __restri
     }
 }
 
+// Q8_0 caches on the bf16 MFMAs: an int8 value is exact in bf16 and bf16
+// has fp32's exponent range, so P times the per-key V scale needs no
+// rescaling.  The cache rows (68-byte head rows) are loaded as words; K is
+// widened to bf16 in registers, V is widened and staged in LDS in the 16-bit
+// layout above.
+template <int KV>
+struct MTileQ8 {
+    static constexpr int ROWB = KV * kQ8HeadBytes;        // cache bytes per row
+    static constexpr int NKB = 2 * KV;                    // one Q8_0 block per 32-dim block
+    static constexpr int NMB = 4 * KV;
+    static constexpr int NVU = kMTileRows * KV * 4 / 64;  // 16-value V runs per lane per tile
+    unsigned k[NKB][2];  // K-block b of key l % 16: dims 8 g .. 8 g + 7 (int8)
+    unsigned v[NVU][4];  // 16 int8 V values
+    unsigned ksc, vsc;   // d0 | d1 << 16 of key l % 16, kv head min(l / 16, KV - 1)
+};
+
+template <int KV>
+__device__ __forceinline__ void mtile_load_q8(MTileQ8<KV>& t, const char* __restrict__ kbase,
+                                              const char* __restrict__ vbase, int valid, int lane) {
+    using Tile = MTileQ8<KV>;
+    constexpr int ROWB = Tile::ROWB;
+    const int col = lane & 15, g = lane >> 4;
+    const int kr = min(col, valid - 1);
+#pragma unroll
+    for (int b = 0; b < Tile::NKB; ++b) {
+        const char* p = kbase + kr * ROWB + (b / 2) * kQ8HeadBytes + 32 * (b % 2) + 8 * g;
+        t.k[b][0] = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p));
+        t.k[b][1] = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p + 4));
+    }
+#pragma unroll
+    for (int i = 0; i < Tile::NVU; ++i) {
+        const int q = 64 * i + lane, r = min(q / (4 * KV), valid - 1), h = (q / 4) % KV, ck = q % 4;
+        const char* p = vbase + r * ROWB + h * kQ8HeadBytes + 16 * ck;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t.v[i][j] = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p + 4 * j));
+    }
+    const int sr = min(col, valid - 1), sh = min(g, KV - 1);
+    t.ksc = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(kbase + sr * ROWB + sh * kQ8HeadBytes + 64));
+    t.vsc = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(vbase + sr * ROWB + sh * kQ8HeadBytes + 64));
+}
+
+// Four int8 (one word) -> four bf16 (two words, element 2i in the low half), exactly.
+__device__ __forceinline__ u32x2 i8x4_to_bf16(unsigned w) {
+    const float f0 = (float)(signed char)w, f1 = (float)(signed char)(w >> 8);
+    const float f2 = (float)(signed char)(w >> 16), f3 = (float)(signed char)(w >> 24);
+    return u32x2{__builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u),
+                 __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u)};
+}
+
+// Element type -> MFMA operand type, tile, and cache row bytes.
+template <typename T, int KV>
+struct MTraits {
+    using Ops = MMath<T>;
+    using Tile = MTile<T, KV>;
+    static constexpr int kCacheRowBytes = Tile::ROWB;
+};
+template <int KV>
+struct MTraits<q8_0_t, KV> {
+    using Ops = MMath<__bf16>;
+    using Tile = MTileQ8<KV>;
+    static constexpr int kCacheRowBytes = Tile::ROWB;
+};
+
+template <typename T, int KV>
+__device__ __forceinline__ void mtile_load_any(typename MTraits<T, KV>::Tile& t, const char* kbase,
+                                               const char* vbase, int valid, int lane) {
+    if constexpr (__is_same(T, q8_0_t))
+        mtile_load_q8<KV>(t, kbase, vbase, valid, lane);
+    else
+        mtile_load<T, KV>(t, kbase, vbase, valid, lane);
+}
+
 template <typename T, int G, int KV, int MODE>
 __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
-    using Tile = MTile<T, KV>;
-    using M = MMath<T>;
-    constexpr int ROWB = Tile::ROWB, CPR = Tile::CPR, NKB = Tile::NKB, NMB = Tile::NMB;
+    constexpr bool Q8 = __is_same(T, q8_0_t);
+    using Tile = typename MTraits<T, KV>::Tile;
+    using M = typename MTraits<T, KV>::Ops;
+    constexpr int ROWC = MTraits<T, KV>::kCacheRowBytes;  // cache bytes per row
+    constexpr int ROWB = KV * kHeadDim * 2;                // bytes per row of the 16-bit LDS V tile
+    constexpr int CPR = ROWB / 16, NKB = 2 * KV, NMB = 4 * KV;
     constexpr int NH = KV * G;
     constexpr int NW = kMWaves, D = kMDepth;
     constexpr bool PAGED = is_paged(MODE);
@@ -1665,12 +1740,24 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     // This wave's LDS copy of the current V tile, and its lane offsets.
     __shared__ __attribute__((aligned(16))) char s_v[NW][kMTileRows * ROWB];
     char* sv = s_v[wave];
-    int wr_off[Tile::NV];
+    constexpr int NWR = Q8 ? 2 * MTileQ8<KV>::NVU : MTile<__bf16, KV>::NV;  // 16-byte LDS writes per lane
+    int wr_off[NWR];
 #pragma unroll
-    for (int i = 0; i < Tile::NV; ++i) {
-        const int q = 64 * i + lane, r = q / CPR, c = q % CPR;
+    for (int i = 0; i < NWR; ++i) {
+        int r, c;
+        if (Q8) {  // run i / 2 of 16 values: row q / (4 KV), kv head (q / 4) % KV, 16-value run q % 4
+            const int q = 64 * (i / 2) + lane;
+            r = q / (4 * KV);
+            c = 8 * ((q / 4) % KV) + 2 * (q % 4) + (i & 1);
+        } else {
+            const int q = 64 * i + lane;
+            r = q / CPR;
+            c = q % CPR;
+        }
         wr_off[i] = r * ROWB + 16 * (c ^ mswz<KV>(r));
     }
+    // Q8_0: per-key block scales pass through LDS ([K, V][key][kv head] words).
+    __shared__ unsigned s_sc[Q8 ? NW : 1][2][kMTileRows][KV];
     int rd_off[NMB];
     {
         const int j = col, r = 4 * g + j / 4;
@@ -1684,26 +1771,64 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     for (int mb = 0; mb < NMB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = kNegInf, l = 0.f;
 
-    const char* kc = reinterpret_cast<const char*>(a.k) + (PAGED ? 0 : base * ROWB);
-    const char* vc = reinterpret_cast<const char*>(a.v) + (PAGED ? 0 : base * ROWB);
+    const char* kc = reinterpret_cast<const char*>(a.k) + (PAGED ? 0 : base * ROWC);
+    const char* vc = reinterpret_cast<const char*>(a.v) + (PAGED ? 0 : base * ROWC);
     const PageMap pm{PAGED ? a.block_table + (size_t)seq * a.max_pages : nullptr, r0, a.n_pages};
     unsigned bad = 0;
     auto tile_off = [&](int t) -> size_t {  // byte offset of tile t's row 0 from kc / vc
         const int row = r0 + t * kMTileRows;
-        if (!PAGED) return (size_t)row * ROWB;
-        return (size_t)page_of(pm, row, bad) * kPageRows * ROWB;
+        if (!PAGED) return (size_t)row * ROWC;
+        return (size_t)page_of(pm, row, bad) * kPageRows * ROWC;
     };
 
     // One tile: q.k, online softmax, p.v.  `valid` rows of the tile are real.
     auto compute = [&](const Tile& t, int valid) {
-#pragma unroll
-        for (int i = 0; i < Tile::NV; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t.v[i];
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+        float dv[NKB][4];  // Q8_0: V scale of block b for this lane's keys 4 g + i
+        if constexpr (Q8) {
 #pragma unroll
-        for (int b = 0; b < NKB; ++b)
+            for (int i = 0; i < MTileQ8<KV>::NVU; ++i) {
+                const u32x2 a0 = i8x4_to_bf16(t.v[i][0]), a1 = i8x4_to_bf16(t.v[i][1]);
+                const u32x2 a2 = i8x4_to_bf16(t.v[i][2]), a3 = i8x4_to_bf16(t.v[i][3]);
+                const u32x4 w0 = {a0[0], a0[1], a1[0], a1[1]}, w1 = {a2[0], a2[1], a3[0], a3[1]};
+                *reinterpret_cast<u32x4*>(sv + wr_off[2 * i]) = w0;
+                *reinterpret_cast<u32x4*>(sv + wr_off[2 * i + 1]) = w1;
+            }
+            if (g < KV) {
+                s_sc[wave][0][col][g] = t.ksc;
+                s_sc[wave][1][col][g] = t.vsc;
+            }
+            float dk[NKB][4];
 #pragma unroll
-            for (int part = 2; part >= 0; --part)  // smallest part first
-                s = M::mfma32(t.k[b], qpart[part][b], s);
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int h = 0; h < KV; ++h) {
+                    const unsigned kw = s_sc[wave][0][4 * g + i][h], vw = s_sc[wave][1][4 * g + i][h];
+                    dk[2 * h][i] = half_bits_to_float(kw & 0xffffu);
+                    dk[2 * h + 1][i] = half_bits_to_float(kw >> 16);
+                    dv[2 * h][i] = half_bits_to_float(vw & 0xffffu);
+                    dv[2 * h + 1][i] = half_bits_to_float(vw >> 16);
+                }
+#pragma unroll
+            for (int b = 0; b < NKB; ++b) {
+                const u32x2 k0 = i8x4_to_bf16(t.k[b][0]), k1 = i8x4_to_bf16(t.k[b][1]);
+                const u32x4 kw = {k0[0], k0[1], k1[0], k1[1]};
+                const bf16x8 kop = __builtin_bit_cast(bf16x8, kw);
+                f32x4 sb = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int part = 2; part >= 0; --part) sb = M::mfma32(kop, qpart[part][b], sb);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[i] = __builtin_fmaf(dk[b][i], sb[i], s[i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NWR; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t.v[i];
+#pragma unroll
+            for (int b = 0; b < NKB; ++b)
+#pragma unroll
+                for (int part = 2; part >= 0; --part)  // smallest part first
+                    s = M::mfma32(t.k[b], qpart[part][b], s);
+        }
         if (M::kScaleQ) s *= s_unscale;
         if (valid < kMTileRows) {
 #pragma unroll
@@ -1726,20 +1851,31 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
             p[i] = fast_exp2(s[i] - m);  // 0 for masked keys
             l += p[i];
         }
-        u32x2 ph, pl;  // P^T (times kPScale) as 16-bit hi + lo
+        // P^T (times kPScale; Q8_0: times the key's V scale of the block) as 16-bit hi + lo
+        constexpr int NP = Q8 ? NKB : 1;
+        typename M::v4 bh[NP], bl[NP];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float p0 = p[2 * i] * M::kPScale, p1 = p[2 * i + 1] * M::kPScale;
-            ph[i] = M::pack2(p0, p1);
-            pl[i] = M::pack2(p0 - M::lo(ph[i]), p1 - M::hi(ph[i]));
+        for (int b = 0; b < NP; ++b) {
+            u32x2 ph, pl;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float p0 = p[2 * i] * M::kPScale, p1 = p[2 * i + 1] * M::kPScale;
+                if constexpr (Q8) {
+                    p0 *= dv[b][2 * i];
+                    p1 *= dv[b][2 * i + 1];
+                }
+                ph[i] = M::pack2(p0, p1);
+                pl[i] = M::pack2(p0 - M::lo(ph[i]), p1 - M::hi(ph[i]));
+            }
+            bh[b] = __builtin_bit_cast(typename M::v4, ph);
+            bl[b] = __builtin_bit_cast(typename M::v4, pl);
         }
-        const typename M::v4 bh = __builtin_bit_cast(typename M::v4, ph);
-        const typename M::v4 bl = __builtin_bit_cast(typename M::v4, pl);
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
             const typename M::v4 va = M::read_tr(sv + rd_off[mb]);
-            acc[mb] = M::mfma16(va, bh, acc[mb]);
-            acc[mb] = M::mfma16(va, bl, acc[mb]);
+            const int b = Q8 ? mb / 2 : 0;  // Q8_0 block of dims 16 mb .. 16 mb + 15
+            acc[mb] = M::mfma16(va, bh[b], acc[mb]);
+            acc[mb] = M::mfma16(va, bl[b], acc[mb]);
         }
     };
 
@@ -1750,7 +1886,7 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const size_t off = tile_off(wave + NW * min(d, nk - 1));
-            mtile_load<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+            mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
             __builtin_amdgcn_sched_barrier(0);
         }
         for (int k0 = 0; k0 < nk; k0 += D) {
@@ -1758,7 +1894,7 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
             for (int d = 0; d < D; ++d) {
                 if (k0 + d < nk) compute(buf[d], kMTileRows);
                 const size_t off = tile_off(wave + NW * min(k0 + d + D, nk - 1));
-                mtile_load<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+                mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
             }
         }
     }
@@ -1766,7 +1902,7 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     if (tail > 0 && (full % NW) == wave) {
         Tile t;
         const size_t off = tile_off(full);
-        mtile_load<T, KV>(t, kc + off, vc + off, tail, lane);
+        mtile_load_any<T, KV>(t, kc + off, vc + off, tail, lane);
         compute(t, tail);
     }
     if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
@@ -1820,7 +1956,8 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     }
 #define TMAC_MDECODE_KERNELS(G, KV)               \
     TMAC_MDECODE_KERNELS_T(G, KV, bf16, __bf16)    \
-    TMAC_MDECODE_KERNELS_T(G, KV, f16, _Float16)
+    TMAC_MDECODE_KERNELS_T(G, KV, f16, _Float16)   \
+    TMAC_MDECODE_KERNELS_T(G, KV, q8, q8_0_t)
 
 #if TMAC_IN_PART(3)
 TMAC_MDECODE_KERNELS(7, 2)

@@ -107,7 +107,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head_n[kNarrowTypes][3];    // the same: head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> paged[4][2];  // paged caches by kv_dtype: decode, layer step
     std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
-    std::map<std::pair<int, int>, hipFunction_t> mdecode[2][3];  // MFMA decode (bf16, fp16): uniform, ragged, paged
+    std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][3];  // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
@@ -215,9 +215,9 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
             k->head = nullptr;
             k->combine = ctx->combine_p[paged].at({g, n_kv_head});
         }
-        // bf16 / fp16 decode (not the layer step) on the MFMA kernel where one is built for the shape.
+        // Narrow-cache decode (not the layer step) on the MFMA kernel where one is built for the shape.
         const int mm = paged == kPagedDecode ? 2 : paged < 0 && mode != kModeLayer ? mode : -1;
-        if ((dt == TMAC_KV_BF16 || dt == TMAC_KV_F16) && ctx->opt_mfma && mm >= 0) {
+        if (dt != TMAC_KV_F32 && ctx->opt_mfma && mm >= 0) {
             auto& tab = ctx->mdecode[dt - 1][mm];
             auto f = tab.find({g, n_kv_head});
             if (f != tab.end()) {
@@ -472,7 +472,7 @@ int tmac_init(tmac_context** out, int device) {
                     return bail(hip_fail(ctx, e, name));
                 ctx->head_n[dt][m][{sh[0], sh[1]}] = f;
             }
-            for (int dt = 0; dt < 2; dt++) {  // MFMA decode (bf16, fp16): built for some shapes only
+            for (int dt = 0; dt < kNarrowTypes; dt++) {  // MFMA decode (bf16, fp16, Q8_0)
                 const char* mp[3] = {"tmac_mdecode_u", "tmac_mdecode_r", "tmac_mdecode_p"};
                 std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mp[m], kTypeName[dt + 1], sh[0], sh[1]);
                 if (get_function(ctx, &f, name) == hipSuccess) ctx->mdecode[dt][m][{sh[0], sh[1]}] = f;
