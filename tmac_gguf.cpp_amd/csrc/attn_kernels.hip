@@ -1575,43 +1575,51 @@ __device__ __forceinline__ void mtile_load(MTile<T, KV>& t, const char* __restri
 
 // Q8_0 caches on the bf16 MFMAs: an int8 value is exact in bf16 and bf16
 // has fp32's exponent range, so P times the per-key V scale needs no
-// rescaling.  The cache rows (68-byte head rows) are loaded as words; K is
-// widened to bf16 in registers, V is widened and staged in LDS in the 16-bit
-// layout above.
+// rescaling.  A 16-row tile of 68-byte head rows is one contiguous run of
+// 16 * KV * 68 bytes: it is loaded as aligned 16-byte chunks (head rows are
+// only 4-byte aligned, so per-operand loads would be misaligned and many),
+// staged raw in LDS, and the K operands, scales and V runs are read from
+// there; V is widened to bf16 into the 16-bit V tile layout above.
 template <int KV>
 struct MTileQ8 {
-    static constexpr int ROWB = KV * kQ8HeadBytes;        // cache bytes per row
-    static constexpr int NKB = 2 * KV;                    // one Q8_0 block per 32-dim block
+    static constexpr int ROWB = KV * kQ8HeadBytes;  // cache bytes per row
+    static constexpr int RAW = kMTileRows * ROWB;   // bytes per tensor tile
+    static constexpr int NCH = RAW / 16;            // 16-byte chunks per tensor tile
+    static constexpr int NR = (NCH + 63) / 64;      // chunk loads per lane
+    static constexpr int NKB = 2 * KV;
     static constexpr int NMB = 4 * KV;
     static constexpr int NVU = kMTileRows * KV * 4 / 64;  // 16-value V runs per lane per tile
-    unsigned k[NKB][2];  // K-block b of key l % 16: dims 8 g .. 8 g + 7 (int8)
-    unsigned v[NVU][4];  // 16 int8 V values
-    unsigned ksc, vsc;   // d0 | d1 << 16 of key l % 16, kv head min(l / 16, KV - 1)
+    u32x4 k[NR], v[NR];
 };
 
+// A full tile: chunk c = 64 i + lane (the last chunk repeated past the end).
 template <int KV>
 __device__ __forceinline__ void mtile_load_q8(MTileQ8<KV>& t, const char* __restrict__ kbase,
-                                              const char* __restrict__ vbase, int valid, int lane) {
+                                              const char* __restrict__ vbase, int lane) {
     using Tile = MTileQ8<KV>;
-    constexpr int ROWB = Tile::ROWB;
-    const int col = lane & 15, g = lane >> 4;
-    const int kr = min(col, valid - 1);
 #pragma unroll
-    for (int b = 0; b < Tile::NKB; ++b) {
-        const char* p = kbase + kr * ROWB + (b / 2) * kQ8HeadBytes + 32 * (b % 2) + 8 * g;
-        t.k[b][0] = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p));
-        t.k[b][1] = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p + 4));
+    for (int i = 0; i < Tile::NR; ++i) {
+        const int c = min(64 * i + lane, Tile::NCH - 1);
+        t.k[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kbase + 16 * c));
+        t.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + 16 * c));
     }
+}
+
+// A partial tile (valid < 16 rows) straight into the LDS raw areas, word by
+// word, reading only the valid rows' bytes.
+template <int KV>
+__device__ __forceinline__ void mtile_tail_q8(const char* __restrict__ kbase, const char* __restrict__ vbase,
+                                              int valid, char* rk, char* rv, int lane) {
+    using Tile = MTileQ8<KV>;
+    const int n4 = valid * Tile::ROWB / 4;
 #pragma unroll
-    for (int i = 0; i < Tile::NVU; ++i) {
-        const int q = 64 * i + lane, r = min(q / (4 * KV), valid - 1), h = (q / 4) % KV, ck = q % 4;
-        const char* p = vbase + r * ROWB + h * kQ8HeadBytes + 16 * ck;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) t.v[i][j] = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p + 4 * j));
+    for (int i = 0; i < (Tile::RAW / 4 + 63) / 64; ++i) {
+        const int w = 64 * i + lane;
+        if (w < n4) {
+            reinterpret_cast<unsigned*>(rk)[w] = reinterpret_cast<const unsigned*>(kbase)[w];
+            reinterpret_cast<unsigned*>(rv)[w] = reinterpret_cast<const unsigned*>(vbase)[w];
+        }
     }
-    const int sr = min(col, valid - 1), sh = min(g, KV - 1);
-    t.ksc = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(kbase + sr * ROWB + sh * kQ8HeadBytes + 64));
-    t.vsc = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(vbase + sr * ROWB + sh * kQ8HeadBytes + 64));
 }
 
 // Four int8 (one word) -> four bf16 (two words, element 2i in the low half), exactly.
@@ -1640,7 +1648,7 @@ template <typename T, int KV>
 __device__ __forceinline__ void mtile_load_any(typename MTraits<T, KV>::Tile& t, const char* kbase,
                                                const char* vbase, int valid, int lane) {
     if constexpr (__is_same(T, q8_0_t))
-        mtile_load_q8<KV>(t, kbase, vbase, valid, lane);
+        mtile_load_q8<KV>(t, kbase, vbase, lane);  // full tiles only (the tail goes through mtile_tail_q8)
     else
         mtile_load<T, KV>(t, kbase, vbase, valid, lane);
 }
@@ -1737,9 +1745,15 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
         for (int part = 0; part < 3; ++part) qpart[part][b] = __builtin_bit_cast(typename M::v8, w[part]);
     }
 
-    // This wave's LDS copy of the current V tile, and its lane offsets.
-    __shared__ __attribute__((aligned(16))) char s_v[NW][kMTileRows * ROWB];
-    char* sv = s_v[wave];
+    // LDS: during the tile loop each wave owns a V tile (16-bit, swizzled) and,
+    // for Q8_0, the raw K and V tiles; after it the same bytes hold the
+    // per-wave states for the merge.
+    constexpr int VT = kMTileRows * ROWB;
+    constexpr int RAWT = Q8 ? MTileQ8<KV>::RAW : 0;
+    constexpr int WAVE_LDS = VT + 2 * RAWT;
+    constexpr int MERGE_LDS = NW * NH * kHeadDim * 4 + 2 * NW * NH * 4;
+    __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_LDS > MERGE_LDS ? NW * WAVE_LDS : MERGE_LDS];
+    char* sv = smem + wave * WAVE_LDS;
     constexpr int NWR = Q8 ? 2 * MTileQ8<KV>::NVU : MTile<__bf16, KV>::NV;  // 16-byte LDS writes per lane
     int wr_off[NWR];
 #pragma unroll
@@ -1756,8 +1770,8 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
         }
         wr_off[i] = r * ROWB + 16 * (c ^ mswz<KV>(r));
     }
-    // Q8_0: per-key block scales pass through LDS ([K, V][key][kv head] words).
-    __shared__ unsigned s_sc[Q8 ? NW : 1][2][kMTileRows][KV];
+    char* rk = sv + VT;    // Q8_0: raw K tile
+    char* rv = rk + RAWT;  // Q8_0: raw V tile
     int rd_off[NMB];
     {
         const int j = col, r = 4 * g + j / 4;
@@ -1782,28 +1796,40 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     };
 
     // One tile: q.k, online softmax, p.v.  `valid` rows of the tile are real.
-    auto compute = [&](const Tile& t, int valid) {
+    // One tile: q.k, online softmax, p.v.  `valid` rows of the tile are real
+    // (Q8_0: the raw tile is already in LDS when t is null).
+    auto compute = [&](const Tile* t, int valid) {
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
         float dv[NKB][4];  // Q8_0: V scale of block b for this lane's keys 4 g + i
         if constexpr (Q8) {
+            constexpr int RB = MTileQ8<KV>::ROWB;
+            if (t) {
 #pragma unroll
-            for (int i = 0; i < MTileQ8<KV>::NVU; ++i) {
-                const u32x2 a0 = i8x4_to_bf16(t.v[i][0]), a1 = i8x4_to_bf16(t.v[i][1]);
-                const u32x2 a2 = i8x4_to_bf16(t.v[i][2]), a3 = i8x4_to_bf16(t.v[i][3]);
+                for (int i = 0; i < MTileQ8<KV>::NR; ++i) {
+                    const int c = min(64 * i + lane, MTileQ8<KV>::NCH - 1);
+                    *reinterpret_cast<u32x4*>(rk + 16 * c) = t->k[i];
+                    *reinterpret_cast<u32x4*>(rv + 16 * c) = t->v[i];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < MTileQ8<KV>::NVU; ++i) {  // V runs: widen to bf16, into the V tile
+                const int q = 64 * i + lane, r = q / (4 * KV), h = (q / 4) % KV, ck = q % 4;
+                const unsigned* src = reinterpret_cast<const unsigned*>(rv + r * RB + h * kQ8HeadBytes + 16 * ck);
+                const u32x2 a0 = i8x4_to_bf16(src[0]), a1 = i8x4_to_bf16(src[1]);
+                const u32x2 a2 = i8x4_to_bf16(src[2]), a3 = i8x4_to_bf16(src[3]);
                 const u32x4 w0 = {a0[0], a0[1], a1[0], a1[1]}, w1 = {a2[0], a2[1], a3[0], a3[1]};
                 *reinterpret_cast<u32x4*>(sv + wr_off[2 * i]) = w0;
                 *reinterpret_cast<u32x4*>(sv + wr_off[2 * i + 1]) = w1;
-            }
-            if (g < KV) {
-                s_sc[wave][0][col][g] = t.ksc;
-                s_sc[wave][1][col][g] = t.vsc;
             }
             float dk[NKB][4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int h = 0; h < KV; ++h) {
-                    const unsigned kw = s_sc[wave][0][4 * g + i][h], vw = s_sc[wave][1][4 * g + i][h];
+                    const int o = (4 * g + i) * RB + h * kQ8HeadBytes + 64;
+                    const bool ok = 4 * g + i < valid;  // rows past the tile's end: weight 0, whatever LDS holds
+                    const unsigned kw = *reinterpret_cast<const unsigned*>(rk + o);
+                    const unsigned vw = ok ? *reinterpret_cast<const unsigned*>(rv + o) : 0u;
                     dk[2 * h][i] = half_bits_to_float(kw & 0xffffu);
                     dk[2 * h + 1][i] = half_bits_to_float(kw >> 16);
                     dv[2 * h][i] = half_bits_to_float(vw & 0xffffu);
@@ -1811,7 +1837,9 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
                 }
 #pragma unroll
             for (int b = 0; b < NKB; ++b) {
-                const u32x2 k0 = i8x4_to_bf16(t.k[b][0]), k1 = i8x4_to_bf16(t.k[b][1]);
+                const unsigned* src =
+                    reinterpret_cast<const unsigned*>(rk + col * RB + (b / 2) * kQ8HeadBytes + 32 * (b % 2) + 8 * g);
+                const u32x2 k0 = i8x4_to_bf16(src[0]), k1 = i8x4_to_bf16(src[1]);
                 const u32x4 kw = {k0[0], k0[1], k1[0], k1[1]};
                 const bf16x8 kop = __builtin_bit_cast(bf16x8, kw);
                 f32x4 sb = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1822,12 +1850,12 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < NWR; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t.v[i];
+            for (int i = 0; i < NWR; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t->v[i];
 #pragma unroll
             for (int b = 0; b < NKB; ++b)
 #pragma unroll
                 for (int part = 2; part >= 0; --part)  // smallest part first
-                    s = M::mfma32(t.k[b], qpart[part][b], s);
+                    s = M::mfma32(t->k[b], qpart[part][b], s);
         }
         if (M::kScaleQ) s *= s_unscale;
         if (valid < kMTileRows) {
@@ -1892,7 +1920,7 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
         for (int k0 = 0; k0 < nk; k0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                if (k0 + d < nk) compute(buf[d], kMTileRows);
+                if (k0 + d < nk) compute(&buf[d], kMTileRows);
                 const size_t off = tile_off(wave + NW * min(k0 + d + D, nk - 1));
                 mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
             }
@@ -1900,10 +1928,15 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     }
     const int tail = n_rows - full * kMTileRows;
     if (tail > 0 && (full % NW) == wave) {
-        Tile t;
         const size_t off = tile_off(full);
-        mtile_load_any<T, KV>(t, kc + off, vc + off, tail, lane);
-        compute(t, tail);
+        if constexpr (Q8) {
+            mtile_tail_q8<KV>(kc + off, vc + off, tail, rk, rv, lane);
+            compute(nullptr, tail);
+        } else {
+            Tile t;
+            mtile_load_any<T, KV>(t, kc + off, vc + off, tail, lane);
+            compute(&t, tail);
+        }
     }
     if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
 
@@ -1915,9 +1948,10 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) acc[mb] *= 1.0f / M::kPScale;
     }
-    __shared__ float s_acc[NW][NH][kHeadDim];
-    __shared__ float s_m[NW][NH];
-    __shared__ float s_l[NW][NH];
+    __syncthreads();  // every wave is done with its tiles before the merge area reuses them
+    auto s_acc = reinterpret_cast<float (*)[NH][kHeadDim]>(smem);
+    auto s_m = reinterpret_cast<float (*)[NH]>(smem + NW * NH * kHeadDim * 4);
+    auto s_l = reinterpret_cast<float (*)[NH]>(smem + NW * NH * kHeadDim * 4 + NW * NH * 4);
     if (col < NH) {
         const int kv = col / G;
 #pragma unroll
