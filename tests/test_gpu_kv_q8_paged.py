@@ -146,6 +146,65 @@ def test_layer_step_q8(ctx, pos, kernel):
     assert_close(dout.numpy(), ref, f"layer q8 pos={pos}")
 
 
+def rows_of(x: np.ndarray, dt: int, rb: int) -> np.ndarray:
+    """fp32 values -> stored cache rows of rb elements, for any number of kv heads."""
+    flat = np.ascontiguousarray(x, np.float32).reshape(-1)
+    if dt == Q8:
+        return oracle.q8_kv_rows(flat.reshape(-1, HD)).reshape(-1, rb)
+    # the 16-bit casts are elementwise: pad to whole 128-value rows for store()
+    pad = np.concatenate([flat, np.zeros(-flat.size % KVD, np.float32)])
+    return store(pad, dt).reshape(-1)[:flat.size].reshape(-1, rb)
+
+
+def values_of(rows: np.ndarray, dt: int, width: int) -> np.ndarray:
+    """Stored cache rows -> fp32 values [n, width], exactly."""
+    flat = np.ascontiguousarray(rows).reshape(-1)
+    if dt == Q8:
+        return oracle.q8_kv_widen(flat.reshape(-1, oracle.Q8_HEAD_BYTES)).reshape(-1, width)
+    pad = np.concatenate([flat, np.zeros(-flat.size % KVD, flat.dtype)])
+    return widen(pad, dt).reshape(-1)[:flat.size].reshape(-1, width)
+
+
+@pytest.mark.parametrize("dt", ALL_DT)
+@pytest.mark.parametrize("mfma", [0, 1])
+@pytest.mark.parametrize("pos,split_len", [(40, 64), (1500, 0), (333, 16)])
+@pytest.mark.parametrize("g,kv", [(7, 2), (8, 1), (2, 2)])
+def test_layer_step_reused_workspace(ctx, dt, mfma, pos, split_len, g, kv):
+    """The layer step twice in a row with different data: the second call's
+    split partials land on the first call's (every head of every split must be
+    rewritten) and the output starts as NaN (every element must be written),
+    one split (direct output) and several."""
+    nh, kvd, cap = g * kv, kv * HD, pos + 20
+    rb = kv * oracle.Q8_HEAD_BYTES if dt == Q8 else kvd
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_GROUP)
+    ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, mfma)
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, split_len)
+    try:
+        for call in range(2):
+            s = 7000 + 10 * call + pos
+            q, kn, vn = data(s, nh * HD), data(s + 1, kvd), data(s + 2, kvd)
+            k_all, v_all = data(s + 3, (cap, kvd), 2), data(s + 4, (cap, kvd), 2)
+            kb, vb = rows_of(k_all, dt, rb), rows_of(v_all, dt, rb)
+            dq, dkn, dvn = ctx.upload(q), ctx.upload(kn), ctx.upload(vn)
+            dk, dv = ctx.upload(kb), ctx.upload(vb)
+            dout = ctx.upload(np.full(nh * HD, np.nan, np.float32))
+            ctx.layer_attention(dq, dkn, dvn, dk, dv, dout, nh, kv, HD, pos, cap, 1e6, kv_dtype=dt)
+            qr, kr = oracle.rope(q, kn, nh, kv, HD, pos, 1e6)
+            kw, vw = values_of(kb, dt, kvd), values_of(vb, dt, kvd)
+            kw[pos] = values_of(rows_of(kr, dt, rb), dt, kvd)[0]
+            vw[pos] = values_of(rows_of(vn, dt, rb), dt, kvd)[0]
+            np.testing.assert_array_equal(dk.numpy()[pos], rows_of(kr, dt, rb)[0])
+            np.testing.assert_array_equal(dv.numpy()[pos], rows_of(vn, dt, rb)[0])
+            ref = oracle.attention(qr, kw, vw, nh, kv, HD, pos)
+            assert_close(dout.numpy(), ref, f"layer dt={dt} mfma={mfma} pos={pos} split={split_len} g={g} kv={kv} "
+                                            f"call={call}")
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, 1)
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+    assert ctx.check_device_error() == 0
+
+
 def test_graph_replay_q8(ctx):
     L, cap, S = 3, 64, 8
     rb = NKV * oracle.Q8_HEAD_BYTES

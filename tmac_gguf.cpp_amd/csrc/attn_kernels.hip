@@ -494,14 +494,15 @@ __device__ __forceinline__ void attend_rows(const char* __restrict__ kb, const c
     }
 }
 
-// Merges NW per-wave partial states (acc over 64 dims, base-2 max m, sum l)
-// held in LDS, one thread per (head, dim), and writes the output (single
-// split) or this split's (acc, m, l) partial.  The caller synchronizes first.
-template <int NH, int NW>
+// Merges NW partial states (acc over 64 dims, base-2 max m, sum l) held in
+// LDS, one thread per (head, dim) with the block's NT threads striding over
+// them, and writes the output (single split) or this split's (acc, m, l)
+// partial.  The caller synchronizes first.
+template <int NH, int NW, int NT>
 __device__ __forceinline__ void merge_waves(const float (*s_acc)[NH][kHeadDim], const float (*s_m)[NH],
                                             const float (*s_l)[NH], bool direct, float* __restrict__ out_heads,
                                             float* __restrict__ ws_split) {
-    for (int idx = threadIdx.x; idx < NH * kHeadDim; idx += NW * 64) {
+    for (int idx = threadIdx.x; idx < NH * kHeadDim; idx += NT) {
         const int h = idx >> 6, d = idx & 63;
         float M = kNegInf;
 #pragma unroll
@@ -564,7 +565,7 @@ __device__ __forceinline__ void finish(State<G>& st, int lane, int wave, bool di
         }
     }
     __syncthreads();
-    merge_waves<NH, NW>(s_acc, s_m, s_l, direct, out_heads, ws_split);
+    merge_waves<NH, NW, NW * 64>(s_acc, s_m, s_l, direct, out_heads, ws_split);
 }
 
 // Rows attended by sequence `seq` (n_pos) and its first cache row (base;
@@ -1462,7 +1463,10 @@ TMAC_PREFILL_PACK_KERNEL(4)
 // the VALU only does the softmax, four values per lane per 16-row tile.
 //
 // Same workgroups as the group kernel: grid (split, sequence) or the flat unit
-// grid, 8 waves, the same splits, combine and page addressing.  Wave w takes
+// grid, 8 waves, the same splits, combine and page addressing.  In the layer
+// modes the query is rotated before it is split, and the new token (RoPE,
+// rounding to the cache type and the cache write exactly as the VALU kernels
+// do them) is attended as one more partial in the merge.  Wave w takes
 // the 16-row tiles w, w + 8, ... of its range.  Per tile (16 positions):
 //   S^T (16 keys x 16 columns) = K (16 x KV*64) . Qbd^T.  Column c < n_head is
 //     query head c; Qbd is block diagonal, so column c only meets the 64 dims
@@ -1664,19 +1668,26 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     constexpr int NH = KV * G;
     constexpr int NW = kMWaves, D = kMDepth;
     constexpr bool PAGED = is_paged(MODE);
+    constexpr bool LAYER = is_layer(MODE);
     static_assert(NH <= 16, "query heads are the 16 MFMA columns");
-    static_assert(!is_layer(MODE), "the layer step runs on the VALU kernels");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, g = lane >> 4;
     int split = blockIdx.x, seq = blockIdx.y;
     if (MODE == kRagged || PAGED) {
-        if (!ragged_unit(a.lengths, 0, a.n_seq, a.split_len, a.n_splits, blockIdx.x, seq, split)) return;
+        const bool by_pos = MODE == kPagedLayer;
+        if (!ragged_unit(by_pos ? a.positions : a.lengths, by_pos ? 1 : 0, a.n_seq, a.split_len, a.n_splits,
+                         blockIdx.x, seq, split))
+            return;
     }
     int n_pos, pos;
     size_t base;
-    seq_geometry<MODE>(a, seq, n_pos, pos, base);
+    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) {
+        if (split == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
+        return;
+    }
     n_pos = __builtin_amdgcn_readfirstlane(n_pos);
+    pos = __builtin_amdgcn_readfirstlane(pos);
     float* out_heads = a.out + (size_t)seq * NH * kHeadDim;
     if (n_pos <= 0) {
         if (split == 0)
@@ -1693,7 +1704,9 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     }
     if (split >= n_act) return;
     const int r0 = split * a.split_len;
-    const int n_rows = min(r0 + a.split_len, n_pos) - r0;
+    const int mem_rows = LAYER ? pos : n_pos;  // layer modes: row `pos` is the new token, attended from registers
+    const int n_rows = max(min(r0 + a.split_len, mem_rows) - r0, 0);
+    const float2* cs_row = LAYER ? a.rope_cs + (size_t)pos * (kHeadDim / 2) : nullptr;
 
     // Q^T operands: column col, dims 32 (b % 2) + 8 g + 0..7 of kv head b / 2,
     // zero unless head col belongs to that kv head.  Three 16-bit parts (hi +
@@ -1706,7 +1719,15 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
         const float* qp = a.q + ((size_t)seq * NH + min(col, NH - 1)) * kHeadDim + 32 * (b % 2) + 8 * g;
         const float4 x0 = *reinterpret_cast<const float4*>(qp);
         const float4 x1 = *reinterpret_cast<const float4*>(qp + 4);
-        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        if (LAYER) {  // RoPE of pairs (16 (b % 2) + 4 g + t)
+            const float4 c0 = *reinterpret_cast<const float4*>(cs_row + 16 * (b % 2) + 4 * g);
+            const float4 c1 = *reinterpret_cast<const float4*>(cs_row + 16 * (b % 2) + 4 * g + 2);
+            rotate_pair(x[0], x[1], c0.x, c0.y);
+            rotate_pair(x[2], x[3], c0.z, c0.w);
+            rotate_pair(x[4], x[5], c1.x, c1.y);
+            rotate_pair(x[6], x[7], c1.z, c1.w);
+        }
 #pragma unroll
         for (int t = 0; t < 8; ++t) qx[b][t] = mine ? x[t] * a.qscale : 0.f;
     }
@@ -1751,7 +1772,8 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     constexpr int VT = kMTileRows * ROWB;
     constexpr int RAWT = Q8 ? MTileQ8<KV>::RAW : 0;
     constexpr int WAVE_LDS = VT + 2 * RAWT;
-    constexpr int MERGE_LDS = NW * NH * kHeadDim * 4 + 2 * NW * NH * 4;
+    constexpr int NP = NW + (LAYER ? 1 : 0);  // partials merged: the waves, plus the new token in layer modes
+    constexpr int MERGE_LDS = NP * NH * kHeadDim * 4 + 2 * NP * NH * 4;
     __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_LDS > MERGE_LDS ? NW * WAVE_LDS : MERGE_LDS];
     char* sv = smem + wave * WAVE_LDS;
     constexpr int NWR = Q8 ? 2 * MTileQ8<KV>::NVU : MTile<__bf16, KV>::NV;  // 16-byte LDS writes per lane
@@ -1950,8 +1972,53 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     }
     __syncthreads();  // every wave is done with its tiles before the merge area reuses them
     auto s_acc = reinterpret_cast<float (*)[NH][kHeadDim]>(smem);
-    auto s_m = reinterpret_cast<float (*)[NH]>(smem + NW * NH * kHeadDim * 4);
-    auto s_l = reinterpret_cast<float (*)[NH]>(smem + NW * NH * kHeadDim * 4 + NW * NH * 4);
+    auto s_m = reinterpret_cast<float (*)[NH]>(smem + NP * NH * kHeadDim * 4);
+    auto s_l = reinterpret_cast<float (*)[NH]>(smem + NP * NH * kHeadDim * 4 + NP * NH * 4);
+    if (LAYER && wave == 0) {
+        // The new token (row pos), as one more partial.  Lanes take the VALU
+        // kernels' layout (8 lanes per kv head, dims {4c..4c+3, 32+4c..}): RoPE
+        // its k, round / quantize k and v_new to the cache type, write them to
+        // the cache row (tmac_gguf.cpp:1090-1091; the last split only) and score
+        // them against the rotated, pre-scaled query of each head of the group.
+        const int c = lane & 7, kvh = lane >> 3;
+        const bool mine = lane < 8 * KV;
+        const bool last = split == n_act - 1;
+        float kf[8], vf[8];
+        if (mine) {
+            const int colf = kvh * kHeadDim + 4 * c;
+            const size_t in = (MODE == kPagedLayer ? (size_t)seq * KV * kHeadDim : 0) + colf;
+            load8(kf, a.k_new + in);
+            load8(vf, a.v_new + in);
+            rope8(kf, cs_row, c);
+            size_t row = (size_t)pos;
+            if (PAGED) row = (size_t)page_of(pm, pos, bad) * kPageRows + (pos & (kPageRows - 1));
+            const int lane_col = kvh * CacheFmt<T>::kHeadBytes + 4 * c * CacheFmt<T>::kDimBytes;
+            put_row<T>(kf, reinterpret_cast<char*>(a.k_out) + row * ROWC + lane_col, c, last);
+            put_row<T>(vf, reinterpret_cast<char*>(a.v_out) + row * ROWC + lane_col, c, last);
+#pragma unroll
+            for (int gq = 0; gq < G; ++gq) {
+                const int h = kvh * G + gq;
+                float qf[8];
+                load8(qf, a.q + ((size_t)seq * NH + h) * kHeadDim + 4 * c);
+                rope8(qf, cs_row, c);
+                float d = 0.f;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) d = fmaf(qf[t] * a.qscale, kf[t], d);
+                d = slot_sum(d);
+                const bool take = last;  // other splits contribute nothing for the new token
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    s_acc[NW][h][4 * c + t] = take ? vf[t] : 0.f;
+                    s_acc[NW][h][32 + 4 * c + t] = take ? vf[4 + t] : 0.f;
+                }
+                if (c == 0) {
+                    s_m[NW][h] = take ? d : kNegInf;
+                    s_l[NW][h] = take ? 1.f : 0.f;
+                }
+            }
+        }
+        if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
+    }
     if (col < NH) {
         const int kv = col / G;
 #pragma unroll
@@ -1972,7 +2039,7 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     __syncthreads();
     const bool direct = (n_act == 1);
     float* ws_split = direct ? nullptr : a.ws + ((size_t)seq * a.n_splits + split) * NH * kPartialStride;
-    merge_waves<NH, NW>(s_acc, s_m, s_l, direct, out_heads, ws_split);
+    merge_waves<NH, NP, NW * 64>(s_acc, s_m, s_l, direct, out_heads, ws_split);
 }
 
 #define TMAC_MDECODE_KERNELS_T(G, KV, TN, T)                                                          \
@@ -1987,6 +2054,14 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_p_##TN##_g##G##_kv##KV(     \
         DecodeArgs a) {                                                                                \
         mdecode_body<T, G, KV, kPaged>(a);                                                             \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_l_##TN##_g##G##_kv##KV(     \
+        DecodeArgs a) {                                                                                \
+        mdecode_body<T, G, KV, kLayer>(a);                                                             \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_pl_##TN##_g##G##_kv##KV(    \
+        DecodeArgs a) {                                                                                \
+        mdecode_body<T, G, KV, kPagedLayer>(a);                                                        \
     }
 #define TMAC_MDECODE_KERNELS(G, KV)               \
     TMAC_MDECODE_KERNELS_T(G, KV, bf16, __bf16)    \

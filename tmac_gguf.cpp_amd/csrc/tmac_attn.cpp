@@ -107,7 +107,8 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head_n[kNarrowTypes][3];    // the same: head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> paged[4][2];  // paged caches by kv_dtype: decode, layer step
     std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
-    std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][3];  // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged
+    // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged, layer, paged layer
+    std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
@@ -215,9 +216,9 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
             k->head = nullptr;
             k->combine = ctx->combine_p[paged].at({g, n_kv_head});
         }
-        // Narrow-cache decode (not the layer step) on the MFMA kernel where one is built for the shape.
-        const int mm = paged == kPagedDecode ? 2 : paged < 0 && mode != kModeLayer ? mode : -1;
-        if (dt != TMAC_KV_F32 && ctx->opt_mfma && mm >= 0) {
+        // Narrow caches: the group kernel is the MFMA kernel where one is built for the shape.
+        const int mm = paged == kPagedDecode ? 2 : paged == kPagedLayer ? 4 : mode == kModeLayer ? 3 : mode;
+        if (dt != TMAC_KV_F32 && ctx->opt_mfma) {
             auto& tab = ctx->mdecode[dt - 1][mm];
             auto f = tab.find({g, n_kv_head});
             if (f != tab.end()) {
@@ -473,10 +474,12 @@ int tmac_init(tmac_context** out, int device) {
                 ctx->head_n[dt][m][{sh[0], sh[1]}] = f;
             }
             for (int dt = 0; dt < kNarrowTypes; dt++) {  // MFMA decode (bf16, fp16, Q8_0)
-                const char* mp[3] = {"tmac_mdecode_u", "tmac_mdecode_r", "tmac_mdecode_p"};
-                std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mp[m], kTypeName[dt + 1], sh[0], sh[1]);
-                if (get_function(ctx, &f, name) == hipSuccess) ctx->mdecode[dt][m][{sh[0], sh[1]}] = f;
-                (void)hipGetLastError();
+                const char* mp[5] = {"tmac_mdecode_u", "tmac_mdecode_r", "tmac_mdecode_p", "tmac_mdecode_l",
+                                     "tmac_mdecode_pl"};
+                for (int mi = m; mi < 5; mi += 3) {  // m = 0, 1, 2 -> modes m and m + 3
+                    std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mp[mi], kTypeName[dt + 1], sh[0], sh[1]);
+                    if (get_function(ctx, &f, name) == hipSuccess) ctx->mdecode[dt][mi][{sh[0], sh[1]}] = f;
+                }
             }
             if (m < 2) {  // paged kernels: m = kPagedDecode, kPagedLayer
                 const char* pp = m == kPagedDecode ? "tmac_decode_p" : "tmac_layer_p";
