@@ -244,6 +244,65 @@ def test_graph_replay_q8(ctx):
     assert ctx.check_device_error() == 0
 
 
+@pytest.mark.parametrize("dt", [tmac_attn.TMAC_KV_F32, tmac_attn.TMAC_KV_BF16, Q8])
+def test_graph_replay_split_layer_step(ctx, dt):
+    """A captured 3-layer step at long context (positions 1500.. read on the
+    device), where every layer spreads its rows over many workgroups and a
+    combine launch merges them; replayed with new inputs, each replay checked
+    against the oracle, the cache rows it wrote bit for bit."""
+    L, cap, P0, S = 3, 1600, 1500, 4
+    rb = NKV * oracle.Q8_HEAD_BYTES if dt == Q8 else KVD
+    ref_k = np.stack([rows_of(data(1500 + l, (cap, KVD), 2), dt, rb) for l in range(L)])
+    ref_v = np.stack([rows_of(data(1600 + l, (cap, KVD), 2), dt, rb) for l in range(L)])
+    kc, vc = ctx.upload(ref_k), ctx.upload(ref_v)
+    dq, dkn, dvn, dout = ctx.empty((L, NH * HD)), ctx.empty((L, KVD)), ctx.empty((L, KVD)), ctx.empty((L, NH * HD))
+    pos = ctx.upload(np.array([P0], np.int32))
+    ctx.rope_prepare(HD, 1e6, cap)
+    s = ctx.stream()
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_GROUP)
+    try:
+        def layer(i):
+            ctx.layer_attention_devpos(dq.at(i * NH * HD), dkn.at(i * KVD), dvn.at(i * KVD), kc.at(i * cap * rb),
+                                       vc.at(i * cap * rb), dout.at(i * NH * HD), NH, NKV, HD, pos, cap, 1e6,
+                                       stream=s, kv_dtype=dt)
+        n_splits = ctx.query_split(1, cap, NH, NKV)[1]
+        assert n_splits > 8, n_splits
+        for i in range(L):  # sizes the split workspace outside capture (and writes row P0; rewritten below)
+            layer(i)
+        ctx.synchronize(s)
+        ctx.step_begin(s)
+        for i in range(L):
+            layer(i)
+        ctx.pos_update(pos, 1, add=True, stream=s)
+        g = ctx.step_end(s)
+        try:
+            for step in range(S):
+                p = P0 + step
+                q, kn, vn = data(1700 + step, (L, NH * HD)), data(1800 + step, (L, KVD)), data(1900 + step, (L, KVD))
+                dq.copy_from(q)
+                dkn.copy_from(kn)
+                dvn.copy_from(vn)
+                ctx.graph_launch(g, s)
+                ctx.synchronize(s)
+                got = dout.numpy()
+                for l in range(L):
+                    qr, kr = oracle.rope(q[l], kn[l], NH, NKV, HD, p, 1e6)
+                    ref_k[l, p] = rows_of(kr, dt, rb)[0]
+                    ref_v[l, p] = rows_of(vn[l], dt, rb)[0]
+                    ref = oracle.attention(qr, values_of(ref_k[l], dt, KVD), values_of(ref_v[l], dt, KVD), NH, NKV,
+                                           HD, p)
+                    assert_close(got[l], ref, f"dt={dt} pos={p} layer={l}")
+            np.testing.assert_array_equal(kc.numpy(), ref_k)
+            np.testing.assert_array_equal(vc.numpy(), ref_v)
+            assert int(pos.numpy()[0]) == P0 + S
+        finally:
+            ctx.graph_destroy(g)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, 0)
+        ctx.destroy_stream(s)
+    assert ctx.check_device_error() == 0
+
+
 def test_q8_storage_error_against_fp32_cache(ctx):
     """Not a parity bar: what storing the cache as Q8_0 does to the output,
     against the fp32 cache (N(0,1) data, 4096 rows)."""
@@ -345,6 +404,102 @@ def test_decode_paged_shared_prefix_and_splits(ctx):
     ref = oracle.attention_ragged(q, np.concatenate(k_rows), np.concatenate(v_rows), offs, lens, NH, NKV, HD,
                                   n_threads=8)
     assert_close(dout.numpy(), ref, "shared prefix")
+    assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("dt", ALL_DT)
+@pytest.mark.parametrize("mfma", [0, 1])
+def test_split_merge_repeated_calls(ctx, dt, mfma):
+    """Many splits per sequence (forced 64-row splits) merged by the combine
+    launch: ragged, paged and batched decode, each called three times in a
+    row with new queries over the same split workspace."""
+    lens = np.array([1, 0, 700, 3001, 64, 65, 1500], np.int32)
+    n_seq = lens.size
+    offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
+    rows = int(lens.sum())
+    kb, vb = store(data(2100 + dt, (rows, KVD), 2), dt), store(data(2101 + dt, (rows, KVD), 2), dt)
+    kw, vw = widen(kb, dt), widen(vb, dt)
+    k_rows = [kb[o:o + n] for o, n in zip(offs, lens)]
+    v_rows = [vb[o:o + n] for o, n in zip(offs, lens)]
+    n_pages = int(sum((l + PR - 1) // PR for l in lens)) + 5
+    kp, table = build_pool(k_rows, dt, n_pages, np.random.default_rng(21))
+    vp, _ = build_pool(v_rows, dt, n_pages, np.random.default_rng(21))
+    dk, dv, doffs, dlens = ctx.upload(kb), ctx.upload(vb), ctx.upload(offs), ctx.upload(lens)
+    dkp, dvp, dtab = ctx.upload(kp), ctx.upload(vp), ctx.upload(table)
+    dout = ctx.empty((n_seq, NH * HD))
+    nz = lens > 0
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 64)
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_GROUP)
+    ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, mfma)
+    try:
+        for call in range(3):
+            q = data(2200 + 10 * dt + call, (n_seq, NH * HD))
+            dq = ctx.upload(q)
+            ref = oracle.attention_ragged(q[nz], kw, vw, offs[nz], lens[nz], NH, NKV, HD, n_threads=8)
+            ctx.decode_ragged(dq, dk, dv, doffs, dlens, dout, n_seq, NH, NKV, HD, int(lens.max()), kv_dtype=dt)
+            got = dout.numpy()
+            assert np.all(got[~nz] == 0)
+            assert_close(got[nz], ref, f"ragged dt={dt} mfma={mfma} call={call}")
+            ctx.decode_paged(dq, dkp, dvp, n_pages, dtab, table.shape[1], dlens, dout, n_seq, NH, NKV, HD,
+                             int(lens.max()), kv_dtype=dt)
+            got = dout.numpy()
+            assert np.all(got[~nz] == 0)
+            assert_close(got[nz], ref, f"paged dt={dt} mfma={mfma} call={call}")
+            # batched: the first 3 x 700 rows as three sequences
+            ctx.decode_batched(dq, dk, dv, dout, 3, NH, NKV, HD, 700, 700, kv_dtype=dt)
+            ref_b = oracle.attention_ragged(q[:3], kw, vw, np.array([0, 700, 1400], np.int64),
+                                            np.full(3, 700, np.int32), NH, NKV, HD, n_threads=8)
+            assert_close(dout.numpy()[:3], ref_b, f"batched dt={dt} mfma={mfma} call={call}")
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, 1)
+    assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("dt", [tmac_attn.TMAC_KV_F32, Q8])
+def test_split_merge_graph_replay(ctx, dt):
+    """A captured ragged decode with many splits per sequence (decode and
+    combine launches), replayed with new queries, with eager calls of the same
+    shape between the replays."""
+    lens = np.array([3001, 64, 1500, 9], np.int32)
+    n_seq = lens.size
+    offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
+    rows = int(lens.sum())
+    kb, vb = store(data(2300, (rows, KVD), 2), dt), store(data(2301, (rows, KVD), 2), dt)
+    kw, vw = widen(kb, dt), widen(vb, dt)
+    dk, dv, doffs, dlens = ctx.upload(kb), ctx.upload(vb), ctx.upload(offs), ctx.upload(lens)
+    dq, dout = ctx.empty((n_seq, NH * HD)), ctx.empty((n_seq, NH * HD))
+    s = ctx.stream()
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 64)
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_GROUP)
+    try:
+        ctx.decode_ragged(dq, dk, dv, doffs, dlens, dout, n_seq, NH, NKV, HD, int(lens.max()), stream=s,
+                          kv_dtype=dt)  # sizes the split workspace outside capture
+        ctx.synchronize(s)
+        ctx.step_begin(s)
+        ctx.decode_ragged(dq, dk, dv, doffs, dlens, dout, n_seq, NH, NKV, HD, int(lens.max()), stream=s,
+                          kv_dtype=dt)
+        g = ctx.step_end(s)
+        try:
+            for rep in range(4):
+                for eager in (False, True):
+                    q = data(2400 + 2 * rep + eager, (n_seq, NH * HD))
+                    dq.copy_from(q)
+                    if eager:
+                        ctx.decode_ragged(dq, dk, dv, doffs, dlens, dout, n_seq, NH, NKV, HD, int(lens.max()),
+                                          stream=s, kv_dtype=dt)
+                    else:
+                        ctx.graph_launch(g, s)
+                    ctx.synchronize(s)
+                    ref = oracle.attention_ragged(q, kw, vw, offs, lens, NH, NKV, HD, n_threads=8)
+                    assert_close(dout.numpy(), ref, f"dt={dt} replay={rep} eager={eager}")
+        finally:
+            ctx.graph_destroy(g)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, 0)
+        ctx.destroy_stream(s)
     assert ctx.check_device_error() == 0
 
 
