@@ -582,7 +582,7 @@ def main():
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "tmac_decode_u_g7_kv2",
+            "kernel": "tmac_decode_u_g4w_g7_kv2",
             "algorithmic_bytes": c3["bytes"],
         },
         "cpu_baseline": cpu,

@@ -307,7 +307,8 @@ enum tmac_option {
     TMAC_OPT_ROTATE = 4,        /* decode: workgroup w starts w*value steps into its rows (default 0) */
     TMAC_OPT_HEAD_WAVES = 5,    /* head kernel workgroup size in waves: 4, 8 or 16 (default 8) */
     TMAC_OPT_WAVE_ORDER = 6,    /* group kernel: 0 = waves interleave steps, 1 = each wave a contiguous run */
-    TMAC_OPT_GROUP_WAVES = 7,   /* group kernel workgroup size in waves: 4 or 8 (default 8) */
+    TMAC_OPT_GROUP_WAVES = 7,   /* fp32 group kernel workgroup size in waves: 4 or 8; 0 (default) = 4 unless a
+                                   split would hold fewer than 64 rows, then 8 */
     TMAC_OPT_MFMA_DECODE = 8    /* 1 (default): bf16/fp16/Q8_0 caches use the MFMA group kernel (decode and layer step) where one exists; 0: VALU */
 };
 enum tmac_kernel_choice {

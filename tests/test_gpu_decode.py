@@ -137,6 +137,45 @@ def test_decode_ragged(ctx, kernel):
     assert ctx.check_device_error() == 0
 
 
+@pytest.mark.parametrize("waves", [0, 4, 8])
+def test_group_kernel_sizes(ctx, waves):
+    """The fp32 group kernel with 4- and 8-wave workgroups and the automatic
+    choice (4 unless splits would hold under 64 rows): batched shapes on both
+    sides of that line, a ragged batch, and the layer step at long context."""
+    ctx.set_option(tmac_attn.TMAC_OPT_GROUP_WAVES, waves)
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_GROUP)
+    try:
+        for n_seq, n_pos in ((1, 4096), (4, 4096), (40, 777)):
+            k, v = rand_cache(80 + n_seq, n_seq * n_pos)
+            q = oracle.normal(82 + n_seq, (n_seq, NH * HD))
+            offs = np.arange(n_seq, dtype=np.int64) * n_pos
+            ref = oracle.attention_ragged(q, k, v, offs, np.full(n_seq, n_pos, np.int32), NH, NKV, HD,
+                                          n_threads=8)
+            dq, dk, dv, dout = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.empty((n_seq, NH * HD))
+            ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos)
+            assert_close(dout.numpy(), ref, f"batched {n_seq}x{n_pos} waves={waves}")
+            if n_seq == 4:  # the same rows as a ragged batch of unequal lengths
+                lens = np.array([4096, 3000, 1, 2500], np.int32)
+                dl, do = ctx.upload(lens), ctx.upload(offs)
+                ref_r = oracle.attention_ragged(q, k, v, offs, lens, NH, NKV, HD, n_threads=8)
+                ctx.decode_ragged(dq, dk, dv, do, dl, dout, n_seq, NH, NKV, HD, 4096, total_rows=int(lens.sum()))
+                assert_close(dout.numpy(), ref_r, f"ragged waves={waves}")
+        pos, cap = 3000, 3010
+        kc, vc = rand_cache(90, cap)
+        q, kn, vn = oracle.normal(92, NH * HD), oracle.normal(93, KVD), oracle.normal(94, KVD)
+        dq, dkn, dvn = ctx.upload(q), ctx.upload(kn), ctx.upload(vn)
+        dkc, dvc, dout = ctx.upload(kc), ctx.upload(vc), ctx.empty(NH * HD)
+        ctx.layer_attention(dq, dkn, dvn, dkc, dvc, dout, NH, NKV, HD, pos, cap, 1e6)
+        ref, _, _ = oracle.layer_step(q, kn, vn, kc, vc, NH, NKV, HD, pos, 1e6)  # writes row pos of kc, vc
+        assert_close(dout.numpy(), ref, f"layer waves={waves}")
+        np.testing.assert_array_equal(dkc.numpy(), kc)
+        np.testing.assert_array_equal(dvc.numpy(), vc)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_GROUP_WAVES, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_AUTO)
+    assert ctx.check_device_error() == 0
+
+
 def test_graph_24_layer_step_replay(ctx):
     """Config 2 slice: a captured 24-layer step replayed for positions 0..S-1
     with the position read on the device, checked against the oracle per step."""

@@ -123,7 +123,7 @@ struct tmac_context {
     int64_t opt_rot_mul = 0;
     int64_t opt_head_waves = 8;
     int64_t opt_blocked = 0;
-    int64_t opt_group_waves = 8;
+    int64_t opt_group_waves = 0;  // 0: automatic (auto_group_waves)
     int64_t opt_mfma = 1;
     std::string last_error;
     char device_name[256] = {0};
@@ -175,6 +175,7 @@ bool capturing(hipStream_t s) {
 
 struct Kernels {
     hipFunction_t group = nullptr, head = nullptr, combine = nullptr;
+    hipFunction_t group4 = nullptr;  // 4-wave group kernel when the size is chosen per call (fp32 caches)
     int head_waves = 16;
     int group_waves = 8;
 };
@@ -199,18 +200,21 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
                     "no kernel for n_head/n_kv_head = " + std::to_string(g) + ", n_kv_head = " +
                         std::to_string(n_kv_head));
     if (k) {
-        k->group_waves = (int)ctx->opt_group_waves;
+        k->group_waves = ctx->opt_group_waves == 4 ? 4 : 8;
         k->group = k->group_waves == 4 ? ctx->decode4[mode].at({g, n_kv_head}) : it->second;
+        if (ctx->opt_group_waves == 0) k->group4 = ctx->decode4[mode].at({g, n_kv_head});
         k->head_waves = (int)ctx->opt_head_waves;
         k->head = (k->head_waves == 8 ? ctx->head8 : k->head_waves == 4 ? ctx->head4 : ctx->head)[mode].at({g, n_kv_head});
         k->combine = ctx->combine[mode].at({g, n_kv_head});
         if (dt != TMAC_KV_F32) {
+            k->group4 = nullptr;
             k->group_waves = 8;
             k->group = ctx->decode_n[dt - 1][mode].at({g, n_kv_head});
             k->head_waves = 8;
             k->head = ctx->head_n[dt - 1][mode].at({g, n_kv_head});
         }
         if (paged >= 0) {
+            k->group4 = nullptr;
             k->group_waves = kGroupWaves;
             k->group = ctx->paged[dt][paged].at({g, n_kv_head});
             k->head = nullptr;
@@ -261,6 +265,19 @@ void choose_split(const tmac_context* ctx, int waves, int n_seq, int n_pos, int 
     *split_len = len;
     *n_splits = (n_pos + len - 1) / len;
     if (*n_splits < 1) *n_splits = 1;
+}
+
+// fp32 group kernel size when TMAC_OPT_GROUP_WAVES is 0 (automatic).  Four
+// waves per workgroup give each wave twice the run of rows and halve the
+// cross-wave merge: config 3 164 vs 166 us, config 4 60.6 vs 63.7 us,
+// 64 x 4096 rows 49 vs 52 us.  Unless a split would then hold fewer than
+// kAuto4MinRows rows (one sequence over all CUs: 16-row splits, twice the
+// partials to combine; 1 x 4096 rows 26 vs 20 us), where 8 waves are used.
+constexpr int kAuto4MinRows = 64;
+int auto_group_waves(const tmac_context* ctx, int n_seq, int rows, int n_kv_head, int64_t total_rows) {
+    int len = 0, n_splits = 0;
+    choose_split(ctx, 4, n_seq, rows, n_kv_head, &len, &n_splits, total_rows);
+    return len >= kAuto4MinRows ? 4 : 8;
 }
 
 // Head kernel for short contexts that would leave most CUs idle otherwise.
@@ -368,8 +385,14 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
         a.ws = nullptr;
         return launch(ctx, k.head, (unsigned)a.n_head, (unsigned)n_seq, k.head_waves * 64, stream, &a);
     }
+    hipFunction_t group = k.group;
+    int waves = k.group_waves;
+    if (k.group4 && auto_group_waves(ctx, n_seq, grid_rows, n_kv_head, total_rows) == 4) {
+        group = k.group4;
+        waves = 4;
+    }
     int split_len = 0, n_splits = 0;
-    choose_split(ctx, k.group_waves, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows);
+    choose_split(ctx, waves, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows);
     a.split_len = split_len;
     a.n_splits = n_splits;
     if (n_splits > 1) {
@@ -385,9 +408,9 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     if (unit_grid) {  // flat unit grid, n_seq * n_splits bounds the unit count
         const int64_t units = (int64_t)n_seq * n_splits;
         if (units > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: too many splits");
-        rc = launch(ctx, k.group, (unsigned)units, 1, k.group_waves * 64, stream, &a);
+        rc = launch(ctx, group, (unsigned)units, 1, waves * 64, stream, &a);
     } else {
-        rc = launch(ctx, k.group, (unsigned)n_splits, (unsigned)n_seq, k.group_waves * 64, stream, &a);
+        rc = launch(ctx, group, (unsigned)n_splits, (unsigned)n_seq, waves * 64, stream, &a);
     }
     if (rc || n_splits == 1) return rc;
     return launch(ctx, k.combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
@@ -1036,7 +1059,8 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
             ctx->opt_blocked = value;
             return TMAC_OK;
         case TMAC_OPT_GROUP_WAVES:
-            if (value != 4 && value != 8) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: group waves must be 4 or 8");
+            if (value != 0 && value != 4 && value != 8)
+                return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: group waves must be 0 (automatic), 4 or 8");
             ctx->opt_group_waves = value;
             return TMAC_OK;
         case TMAC_OPT_HEAD_WAVES:
@@ -1068,7 +1092,9 @@ int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_
         *n_splits = 0;  // 0 = head kernel (one workgroup per query head)
         return TMAC_OK;
     }
-    choose_split(ctx, (int)ctx->opt_group_waves, n_seq, n_pos, n_kv_head, split_len, n_splits);
+    const int waves = ctx->opt_group_waves ? (int)ctx->opt_group_waves
+                                           : auto_group_waves(ctx, n_seq, n_pos, n_kv_head, 0);
+    choose_split(ctx, waves, n_seq, n_pos, n_kv_head, split_len, n_splits);
     return TMAC_OK;
 }
 
