@@ -900,12 +900,16 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
 }
 
 // Log-sum-exp merge of the split partials: one wave per (head, sequence) with
-// more than one active split.  Lanes load the splits' (m, l) in parallel, the
-// per-split weights go to LDS, then lane d sums acc[split][d] in batches of 8
-// independent loads.
+// more than one active split, lane d owning output dim d.  Splits go in
+// chunks of 32 whose loads are all issued before any is used: lane j loads
+// split j's (m, l), every lane its dim of all 32 acc vectors.  The chunk max
+// and the l-weighted sum are wave reductions, and split j's weight reaches
+// every lane by readlane, so a chunk costs one memory latency; later chunks
+// (more than 32 splits) rescale by the running max.
 template <int G, int KV, int MODE>
 __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
-    constexpr int NH = KV * G;
+    constexpr int NH = KV * G, B = 32;
+    constexpr size_t SP = (size_t)NH * kPartialStride;  // floats between splits
     const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
     int n_pos, pos;
     size_t base;
@@ -913,40 +917,37 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     if (n_pos <= 0) return;
     const int n_act = (n_pos + a.split_len - 1) / a.split_len;
     if (n_act <= 1 || n_act > a.n_splits) return;
-    const float* ws = a.ws + (size_t)seq * a.n_splits * NH * kPartialStride + (size_t)h * kPartialStride;
-    constexpr size_t SP = (size_t)NH * kPartialStride;  // floats between splits
-    __shared__ float s_m[kMaxSplits], s_w[kMaxSplits];
-    float mloc = kNegInf;
-    for (int sp = d; sp < n_act; sp += 64) {
-        const float m = ws[sp * SP + kHeadDim];
-        s_m[sp] = m;
-        s_w[sp] = ws[sp * SP + kHeadDim + 1];  // l, replaced by the weight below
-        mloc = fmaxf(mloc, m);
+    const float* ws = a.ws + (size_t)seq * a.n_splits * SP + (size_t)h * kPartialStride;
+    float M = kNegInf, L = 0.f, A = 0.f;
+    for (int c0 = 0; c0 < n_act; c0 += B) {
+        const int n = min(B, n_act - c0);
+        const int sl = c0 + min(d, n - 1);
+        const float ml = ws[(size_t)sl * SP + kHeadDim];
+        const float ll = ws[(size_t)sl * SP + kHeadDim + 1];
+        float aj[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) aj[j] = ws[(size_t)(c0 + min(j, n - 1)) * SP + d];
+        const float mo = d < n ? ml : kNegInf;
+        float cm = mo;
+#pragma unroll
+        for (int mask = 1; mask < 64; mask <<= 1) cm = fmaxf(cm, __shfl_xor(cm, mask));
+        const float nm = fmaxf(M, cm);  // finite: a sequence with rows has a finite score
+        const float sc = (M == kNegInf) ? 0.f : fast_exp2(M - nm);
+        const float w = (mo == kNegInf) ? 0.f : fast_exp2(mo - nm);
+        float lw = d < n ? ll * w : 0.f;
+#pragma unroll
+        for (int mask = 1; mask < 64; mask <<= 1) lw += __shfl_xor(lw, mask);
+        float acc = A * sc;
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+            acc = fmaf(aj[j], j < n ? wj : 0.f, acc);
+        }
+        A = acc;
+        L = fmaf(L, sc, lw);
+        M = nm;
     }
-#pragma unroll
-    for (int mask = 1; mask < 64; mask <<= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, mask));
-    const float M = mloc;
-    float lsum = 0.f;
-    for (int sp = d; sp < n_act; sp += 64) {
-        const float m = s_m[sp];
-        const float sc = (m == kNegInf) ? 0.f : fast_exp2(m - M);
-        lsum = fmaf(s_w[sp], sc, lsum);
-        s_w[sp] = sc;
-    }
-#pragma unroll
-    for (int mask = 1; mask < 64; mask <<= 1) lsum += __shfl_xor(lsum, mask);
-    __syncthreads();
-    float A = 0.f;
-    int sp = 0;
-    for (; sp + 8 <= n_act; sp += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = ws[(sp + u) * SP + d];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) A = fmaf(v[u], s_w[sp + u], A);
-    }
-    for (; sp < n_act; ++sp) A = fmaf(ws[sp * SP + d], s_w[sp], A);
-    a.out[((size_t)seq * NH + h) * kHeadDim + d] = A / lsum;
+    a.out[((size_t)seq * NH + h) * kHeadDim + d] = A / L;
 }
 
 }  // namespace
