@@ -1559,7 +1559,12 @@ __device__ __forceinline__ int mswz(int r) {  // chunk XOR of row r in the LDS c
 }
 
 // Loads one tile: rows `row0 + 0..15` at `base` (the tile's row 0), rows at or
-// past `valid` replaced by row valid - 1 (in bounds, masked later).
+// past `valid` replaced by row valid - 1 (in bounds, masked later).  A K
+// operand load covers 64 bytes of each of 16 rows, so every 128-byte line is
+// read by two consecutive loads: K uses normal loads, which keep the line in
+// L2 for the second one (non-temporal K loads re-fetched part of those lines
+// from HBM: 1.058x the algorithmic bytes against 1.025x, 97 vs 86 us at
+// config 3).  V rows are read whole, 1 KB per load, and stay non-temporal.
 template <typename T, int KV>
 __device__ __forceinline__ void mtile_load(MTile<T, KV>& t, const char* __restrict__ kbase,
                                            const char* __restrict__ vbase, int valid, int lane) {
@@ -1570,7 +1575,7 @@ __device__ __forceinline__ void mtile_load(MTile<T, KV>& t, const char* __restri
     const int kr = min(col, valid - 1);
 #pragma unroll
     for (int b = 0; b < Tile::NKB; ++b)
-        t.k[b] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(kbase + kr * ROWB + 64 * b + 16 * g));
+        t.k[b] = *reinterpret_cast<const v8*>(kbase + kr * ROWB + 64 * b + 16 * g);
 #pragma unroll
     for (int i = 0; i < Tile::NV; ++i) {
         const int q = 64 * i + lane, r = min(q / CPR, valid - 1), c = q % CPR;
@@ -1598,6 +1603,9 @@ struct MTileQ8 {
 };
 
 // A full tile: chunk c = 64 i + lane (the last chunk repeated past the end).
+// K chunks use normal loads (a tile's first and last 128-byte lines are shared
+// with the neighbouring tiles, which other waves read at about the same time:
+// 77 -> 73 us at config 3), V chunks non-temporal loads.
 template <int KV>
 __device__ __forceinline__ void mtile_load_q8(MTileQ8<KV>& t, const char* __restrict__ kbase,
                                               const char* __restrict__ vbase, int lane) {
@@ -1605,7 +1613,7 @@ __device__ __forceinline__ void mtile_load_q8(MTileQ8<KV>& t, const char* __rest
 #pragma unroll
     for (int i = 0; i < Tile::NR; ++i) {
         const int c = min(64 * i + lane, Tile::NCH - 1);
-        t.k[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kbase + 16 * c));
+        t.k[i] = *reinterpret_cast<const u32x4*>(kbase + 16 * c);  // normal: see mtile_load
         t.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + 16 * c));
     }
 }
