@@ -1952,8 +1952,10 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 if (k0 + d < nk) compute(&buf[d], kMTileRows);
-                const size_t off = tile_off(wave + NW * min(k0 + d + D, nk - 1));
-                mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+                if (k0 + d + D < nk) {  // no prefetch past the wave's last tile (1.6% at config 3, bf16)
+                    const size_t off = tile_off(wave + NW * (k0 + d + D));
+                    mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+                }
             }
         }
     }
