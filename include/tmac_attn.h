@@ -342,6 +342,8 @@ int tmac_free(tmac_context* ctx, void* ptr);
 int tmac_memcpy_h2d(tmac_context* ctx, tmac_stream stream, void* dst, const void* src, size_t bytes);
 int tmac_memcpy_d2h(tmac_context* ctx, tmac_stream stream, void* dst, const void* src, size_t bytes);
 int tmac_memcpy_d2d(tmac_context* ctx, tmac_stream stream, void* dst, const void* src, size_t bytes);
+/* tmac_memset returns TMAC_ERR_CAPTURE on a capturing stream: a memset node in a replayed graph has not
+ * reliably cleared memory on replays after the first on this GPU; clear memory before tmac_step_begin. */
 int tmac_memset(tmac_context* ctx, tmac_stream stream, void* dst, int value, size_t bytes);
 int tmac_stream_create(tmac_context* ctx, tmac_stream* stream);
 int tmac_stream_destroy(tmac_context* ctx, tmac_stream stream);

@@ -5,6 +5,8 @@ Oracle = oracle/tmac_oracle.c, the restatement of tmac_gguf.cpp:990-1016 (RoPE),
 outputs: |gpu - ref| <= 2e-5 + 1e-4 |ref| elementwise.  RoPE and the cache
 write are compared bit for bit.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -174,6 +176,29 @@ def test_group_kernel_sizes(ctx, waves):
         ctx.set_option(tmac_attn.TMAC_OPT_GROUP_WAVES, 0)
         ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_AUTO)
     assert ctx.check_device_error() == 0
+
+
+def test_memset_refused_while_capturing(ctx):
+    """tmac_memset on a capturing stream returns TMAC_ERR_CAPTURE and records
+    nothing; the capture stays usable and the captured RoPE replays exactly."""
+    x = oracle.normal(77, 2 * HD)
+    d = ctx.upload(x)
+    s = ctx.stream()
+    ctx.rope_prepare(HD, 1e6, 16)
+    ctx.step_begin(s)
+    try:
+        rc = ctx.lib.tmac_memset(ctx.handle, s, ctypes.c_void_p(d.ptr), 0, d.nbytes)
+        assert rc == tmac_attn.TMAC_ERR_CAPTURE
+        ctx.rope_op(d, 2, HD, 5, 1e6, stream=s)
+    finally:
+        g = ctx.step_end(s)
+    try:
+        ctx.graph_launch(g, s)
+        ctx.synchronize(s)
+        np.testing.assert_array_equal(d.numpy(), oracle.rope_heads(x, 2, HD, 5, 1e6))
+    finally:
+        ctx.graph_destroy(g)
+        ctx.destroy_stream(s)
 
 
 def test_graph_24_layer_step_replay(ctx):

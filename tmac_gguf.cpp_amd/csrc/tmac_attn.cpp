@@ -1207,6 +1207,10 @@ int tmac_memset(tmac_context* ctx, tmac_stream stream, void* dst, int value, siz
     if (rc) return rc;
     if (!bytes) return TMAC_OK;
     if (!dst) return TMAC_ERR_NULL_POINTER;
+    if (capturing((hipStream_t)stream))
+        return fail(ctx, TMAC_ERR_CAPTURE,
+                    "memset: the stream is capturing; a memset node does not reliably clear memory on graph "
+                    "replays, so clear it before tmac_step_begin");
     HIP_TRY(ctx, hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
     return TMAC_OK;
 }
