@@ -298,6 +298,12 @@ int tmac_layer_attention_paged(tmac_context* ctx, tmac_stream stream, int kv_dty
 int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
                            const float* v_cache, float* out, int n_seq, int n_q, int prefix_len,
                            int64_t seq_stride, int n_head, int n_kv_head, int head_dim);
+/* The same over a bf16 / fp16 / Q8_0 cache (tmac_kv_dtype; no counterpart in the
+ * reference, whose cache is fp32): rows are widened exactly to fp32 and then rounded
+ * to bf16 like the fp32 rows (exact for a bf16 cache). */
+int tmac_attention_prefill_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                              const void* k_cache, const void* v_cache, float* out, int n_seq, int n_q,
+                              int prefix_len, int64_t seq_stride, int n_head, int n_kv_head, int head_dim);
 
 /* ---- tuning / introspection ---- */
 enum tmac_option {

@@ -78,6 +78,41 @@ def test_prefill_config5_sampled_rows(ctx):
     assert_close(np.concatenate([got[s, rows] for s in range(n_seq)]), ref, "config 5 sampled rows")
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16", "q8"])
+@pytest.mark.parametrize("n_seq,n_q,prefix,n_head,n_kv", [(2, 37, 100, 14, 2), (1, 33, 200, 16, 4),
+                                                          (2, 20, 50, 8, 1), (1, 5, 0, 14, 2)])
+def test_prefill_narrow_caches(ctx, dt, n_seq, n_q, prefix, n_head, n_kv):
+    """tmac_attention_prefill_kv over a bf16 / fp16 / Q8_0 cache: the rows are
+    widened exactly to fp32, then rounded to bf16 like fp32 rows, so the
+    reference is the oracle on those widened, rounded rows."""
+    import tmac_attn
+    cap = prefix + n_q + 3
+    q, k, v = make(800 + n_q, n_seq, n_q, prefix, cap, n_head, n_kv)
+    q = bf16_round(q)
+    kvd = n_kv * HD
+    if dt == "bf16":
+        code = tmac_attn.TMAC_KV_BF16
+        store = lambda x: (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+        widen = lambda b: (b.astype(np.uint32) << 16).view(np.float32)
+    elif dt == "f16":
+        code = tmac_attn.TMAC_KV_F16
+        store = lambda x: x.astype(np.float16).view(np.uint16)
+        widen = lambda b: b.view(np.float16).astype(np.float32)
+    else:
+        code = tmac_attn.TMAC_KV_Q8_0
+        store = lambda x: oracle.q8_kv_rows(x.reshape(-1, HD)).reshape(n_seq, cap, n_kv * oracle.Q8_HEAD_BYTES)
+        widen = lambda b: oracle.q8_kv_widen(b).reshape(n_seq, cap, kvd)
+    kb, vb = store(k), store(v)
+    kw, vw = bf16_round(widen(kb).reshape(n_seq, cap, kvd)), bf16_round(widen(vb).reshape(n_seq, cap, kvd))
+    dq, dk, dv = ctx.upload(q), ctx.upload(kb), ctx.upload(vb)
+    out = ctx.empty((n_seq, n_q, n_head * HD))
+    ctx.prefill(dq, dk, dv, out, n_seq, n_q, prefix, cap, n_head, n_kv, HD, kv_dtype=code)
+    ref = oracle.prefill(q, kw, vw, n_seq, n_q, prefix, cap, n_head, n_kv, HD, n_threads=8)
+    assert_close(out.numpy(), ref, f"prefill {dt} {n_seq}x{n_q} prefix {prefix} heads {n_head}/{n_kv}")
+    assert ctx.prefill(dq, dk, dv, out, n_seq, n_q, prefix, cap, n_head, n_kv, HD, kv_dtype=9,
+                       check=False) == tmac_attn.TMAC_ERR_INVALID_ARG
+
+
 def test_prefill_rejects_bad_arguments(ctx):
     import tmac_attn
     d = ctx.empty(16 * 14 * HD)

@@ -1125,44 +1125,52 @@ __device__ __forceinline__ float sum4_rows(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Pack one 64-row tile of one (sequence, kv head): 256 threads, thread t owns
-// row t / 4 and columns 16 * (t % 4) .. + 15 of the K tile and of the V^T tile.
-// Rows at or past n_rows are written as zeros.
-template <int KV>
+// Pack one 64-row tile of one (sequence, kv head) from a cache of element
+// type T (fp32, bf16, fp16 or Q8_0 head rows): 256 threads, thread t owns row
+// t / 4 and the 8-dim chunks q4 and 4 + q4 (q4 = t % 4) of the K tile and of
+// the V^T tile.  Values are widened exactly to fp32 (load_row) and rounded to
+// bf16 (nearest even; exact for a bf16 cache).  Rows at or past n_rows are
+// written as zeros.
+template <typename T, int KV>
 __device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
-    constexpr int ROW = KV * kHeadDim;
+    constexpr int HB = CacheFmt<T>::kHeadBytes, ROWB = KV * HB, DB = CacheFmt<T>::kDimBytes;
     const int tile = blockIdx.x % a.n_tp;
     const int rest = blockIdx.x / a.n_tp;
     const int kv = rest % KV, seq = rest / KV;
     const int tid = threadIdx.x, r = tid >> 2, q4 = tid & 3;
     const int key = tile * kPrefillKeys + r;
     const size_t row = (size_t)seq * a.seq_stride + (size_t)min(key, a.n_rows - 1);
-    const float* kp = a.k + row * ROW + kv * kHeadDim + 16 * q4;
-    const float* vp = a.v + row * ROW + kv * kHeadDim + 16 * q4;
+    const char* kh = reinterpret_cast<const char*>(a.k) + row * ROWB + kv * HB;
+    const char* vh = reinterpret_cast<const char*>(a.v) + row * ROWB + kv * HB;
     const bool valid = key < a.n_rows;
     __shared__ float sv[64][65];
-    float kx[16];
+    // load_row(c) gives dims 4c..4c+3 and 32+4c..32+4c+3; c = 2 q4 and 2 q4 + 1
+    // together hold the chunks 8 q4 .. 8 q4 + 7 and 32 + 8 q4 .. 32 + 8 q4 + 7.
+    float k0[8], k1[8], v0[8], v1[8];
+    load_row<T, false>(k0, kh + 4 * (2 * q4) * DB, 2 * q4);
+    load_row<T, false>(k1, kh + 4 * (2 * q4 + 1) * DB, 2 * q4 + 1);
+    load_row<T, false>(v0, vh + 4 * (2 * q4) * DB, 2 * q4);
+    load_row<T, false>(v1, vh + 4 * (2 * q4 + 1) * DB, 2 * q4 + 1);
+    float kx[2][8];  // [chunk: 8 q4.., 32 + 8 q4..][dim]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 kf = *reinterpret_cast<const float4*>(kp + 4 * i);
-        const float4 vf = *reinterpret_cast<const float4*>(vp + 4 * i);
-        kx[4 * i + 0] = valid ? kf.x : 0.f;
-        kx[4 * i + 1] = valid ? kf.y : 0.f;
-        kx[4 * i + 2] = valid ? kf.z : 0.f;
-        kx[4 * i + 3] = valid ? kf.w : 0.f;
-        sv[r][16 * q4 + 4 * i + 0] = valid ? vf.x : 0.f;
-        sv[r][16 * q4 + 4 * i + 1] = valid ? vf.y : 0.f;
-        sv[r][16 * q4 + 4 * i + 2] = valid ? vf.z : 0.f;
-        sv[r][16 * q4 + 4 * i + 3] = valid ? vf.w : 0.f;
+    for (int t = 0; t < 4; ++t) {
+        kx[0][t] = valid ? k0[t] : 0.f;
+        kx[0][4 + t] = valid ? k1[t] : 0.f;
+        kx[1][t] = valid ? k0[4 + t] : 0.f;
+        kx[1][4 + t] = valid ? k1[4 + t] : 0.f;
+        sv[r][8 * q4 + t] = valid ? v0[t] : 0.f;
+        sv[r][8 * q4 + 4 + t] = valid ? v1[t] : 0.f;
+        sv[r][32 + 8 * q4 + t] = valid ? v0[4 + t] : 0.f;
+        sv[r][32 + 8 * q4 + 4 + t] = valid ? v1[4 + t] : 0.f;
     }
     __bf16* dst = reinterpret_cast<__bf16*>(a.packed) +
                   (((size_t)seq * KV + kv) * a.n_tp + tile) * kPrefillTileElems;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
-        const float* x = kx + 8 * cc;
+        const float* x = kx[cc];
         const u32x4 w = {bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3]), bf16_pair(x[4], x[5]),
                          bf16_pair(x[6], x[7])};
-        *reinterpret_cast<u32x4*>(dst + tile_offset(r, 16 * q4 + 8 * cc)) = w;
+        *reinterpret_cast<u32x4*>(dst + tile_offset(r, 32 * cc + 8 * q4)) = w;
     }
     __syncthreads();
     // V^T row d = r, columns p = 16 * q4 .. + 15 hold keys vt_key(p)
@@ -1449,7 +1457,16 @@ TMAC_PREFILL_KERNEL(8, 1)
 
 #define TMAC_PREFILL_PACK_KERNEL(KV)                                                                       \
     extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_kv##KV(PrefillArgs a) {            \
-        prefill_pack_body<KV>(a);                                                                         \
+        prefill_pack_body<float, KV>(a);                                                                  \
+    }                                                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_bf16_kv##KV(PrefillArgs a) {       \
+        prefill_pack_body<__bf16, KV>(a);                                                                 \
+    }                                                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_f16_kv##KV(PrefillArgs a) {        \
+        prefill_pack_body<_Float16, KV>(a);                                                               \
+    }                                                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_q8_kv##KV(PrefillArgs a) {         \
+        prefill_pack_body<q8_0_t, KV>(a);                                                                 \
     }
 TMAC_PREFILL_PACK_KERNEL(1)
 TMAC_PREFILL_PACK_KERNEL(2)

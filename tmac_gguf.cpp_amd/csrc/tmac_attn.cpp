@@ -110,7 +110,7 @@ struct tmac_context {
     // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged, layer, paged layer
     std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
-    std::map<int, hipFunction_t> prefill_pack;                // prefill tile packing, by KV
+    std::map<int, hipFunction_t> prefill_pack[4];             // prefill tile packing, by cache type and KV
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
                   k_kq = nullptr, k_cvt_q8 = nullptr;
     float* ws = nullptr;
@@ -542,11 +542,13 @@ int tmac_init(tmac_context** out, int device) {
                 if ((e = get_function(ctx, &f, name)) != hipSuccess)
                     return bail(hip_fail(ctx, e, name));
                 ctx->prefill[{sh[0], sh[1]}] = f;
-                if (!ctx->prefill_pack.count(sh[1])) {
-                    std::snprintf(name, sizeof(name), "tmac_prefill_pack_kv%d", sh[1]);
+                static const char* const pack_type[4] = {"", "bf16_", "f16_", "q8_"};
+                for (int dt = 0; dt < 4; ++dt) {
+                    if (ctx->prefill_pack[dt].count(sh[1])) continue;
+                    std::snprintf(name, sizeof(name), "tmac_prefill_pack_%skv%d", pack_type[dt], sh[1]);
                     if ((e = get_function(ctx, &f, name)) != hipSuccess)
                         return bail(hip_fail(ctx, e, name));
-                    ctx->prefill_pack[sh[1]] = f;
+                    ctx->prefill_pack[dt][sh[1]] = f;
                 }
             }
         }
@@ -866,11 +868,13 @@ int tmac_kv_convert(tmac_context* ctx, tmac_stream stream, int kv_dtype, const f
     return launch(ctx, ctx->k_cvt16, (unsigned)((n + 255) / 256), 1, 256, (hipStream_t)stream, &a);
 }
 
-int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
-                           const float* v_cache, float* out, int n_seq, int n_q, int prefix_len,
-                           int64_t seq_stride, int n_head, int n_kv_head, int head_dim) {
+static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const float* q, const void* k_cache,
+                        const void* v_cache, float* out, int n_seq, int n_q, int prefix_len, int64_t seq_stride,
+                        int n_head, int n_kv_head, int head_dim) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
+    if (dt != TMAC_KV_F32 && dt != TMAC_KV_BF16 && dt != TMAC_KV_F16 && dt != TMAC_KV_Q8_0)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: kv_dtype must be TMAC_KV_F32, _BF16, _F16 or _Q8_0");
     if (!q || !k_cache || !v_cache || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "prefill: null buffer");
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "prefill: buffers must be 16-byte aligned");
@@ -895,12 +899,27 @@ int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q
     if (pack_blocks > INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: too many cache tiles");
     const size_t pack_bytes = (size_t)pack_blocks * kPrefillTileElems * sizeof(uint16_t);
     if ((rc = ensure_workspace(ctx, (hipStream_t)stream, pack_bytes / sizeof(float)))) return rc;
-    PrefillArgs a{q, k_cache, v_cache, out, seq_stride, n_q, prefix_len, n_qblk, kQScale,
-                  reinterpret_cast<uint16_t*>(ctx->ws), n_tp, n_rows};
-    if ((rc = launch(ctx, ctx->prefill_pack.at(n_kv_head), (unsigned)pack_blocks, 1, 256, (hipStream_t)stream, &a)))
+    PrefillArgs a{q, static_cast<const float*>(k_cache), static_cast<const float*>(v_cache), out, seq_stride, n_q,
+                  prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(ctx->ws), n_tp, n_rows};
+    if ((rc = launch(ctx, ctx->prefill_pack[dt].at(n_kv_head), (unsigned)pack_blocks, 1, 256, (hipStream_t)stream,
+                     &a)))
         return rc;
     return launch(ctx, it->second, (unsigned)((int64_t)n_qblk * n_kv_head * n_seq), 1, kPrefillWaves * 64,
                   (hipStream_t)stream, &a);
+}
+
+int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q, const float* k_cache,
+                           const float* v_cache, float* out, int n_seq, int n_q, int prefix_len,
+                           int64_t seq_stride, int n_head, int n_kv_head, int head_dim) {
+    return prefill_impl(ctx, stream, TMAC_KV_F32, q, k_cache, v_cache, out, n_seq, n_q, prefix_len, seq_stride,
+                        n_head, n_kv_head, head_dim);
+}
+
+int tmac_attention_prefill_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                              const void* k_cache, const void* v_cache, float* out, int n_seq, int n_q,
+                              int prefix_len, int64_t seq_stride, int n_head, int n_kv_head, int head_dim) {
+    return prefill_impl(ctx, stream, kv_dtype, q, k_cache, v_cache, out, n_seq, n_q, prefix_len, seq_stride,
+                        n_head, n_kv_head, head_dim);
 }
 
 int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add) {

@@ -97,6 +97,7 @@ SIGNATURES = {
     "tmac_attention_decode_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
     "tmac_attention_decode_ragged": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
     "tmac_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
+    "tmac_attention_prefill_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_set_option": (_i, [_vp, _i, _i64]),
     "tmac_query_split": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "tmac_check_device_error": (_i, [_vp]),
@@ -489,9 +490,13 @@ class Context:
         return rc
 
     def prefill(self, q, k, v, out, n_seq, n_q, prefix_len, seq_stride, n_head, n_kv_head, head_dim,
-                stream=None, check=True) -> int:
-        rc = self.lib.tmac_attention_prefill(self.handle, stream, _p(q), _p(k), _p(v), _p(out), n_seq, n_q,
-                                             prefix_len, seq_stride, n_head, n_kv_head, head_dim)
+                stream=None, check=True, kv_dtype=TMAC_KV_F32) -> int:
+        if kv_dtype == TMAC_KV_F32:
+            rc = self.lib.tmac_attention_prefill(self.handle, stream, _p(q), _p(k), _p(v), _p(out), n_seq, n_q,
+                                                 prefix_len, seq_stride, n_head, n_kv_head, head_dim)
+        else:
+            rc = self.lib.tmac_attention_prefill_kv(self.handle, stream, kv_dtype, _p(q), _p(k), _p(v), _p(out),
+                                                    n_seq, n_q, prefix_len, seq_stride, n_head, n_kv_head, head_dim)
         if check:
             self._check(rc, "prefill")
         return rc
