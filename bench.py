@@ -54,23 +54,34 @@ def algo_bytes(lengths) -> int:
 
 
 def time_launches(ctx, stream, fn, steps: int, warmup: int):
-    """Runs fn() warmup+steps times on `stream`; returns per-launch ms from
-    HIP events recorded on that stream, and the mean over the timed region."""
+    """Runs fn() `warmup` times untimed, then exactly `steps` times between two
+    HIP events recorded on `stream` (synchronized before and after): the mean
+    over that region is the step time.  A second, instrumented pass of `steps`
+    launches with an event after each gives the per-launch times for the
+    percentiles (an event per launch adds ~2.6 us per launch at config 3, so it
+    stays out of the mean).  Returns (per-launch ms, mean ms)."""
     for _ in range(warmup):
         fn()
     ctx.synchronize(stream)
-    evs = [ctx.event() for _ in range(steps + 1)]
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0, stream)
+    for _ in range(steps):
+        fn()
+    ctx.record(e1, stream)
     ctx.synchronize(stream)
+    mean = ctx.elapsed_ms(e0, e1) / steps
+    ctx.destroy_event(e0)
+    ctx.destroy_event(e1)
+    evs = [ctx.event() for _ in range(steps + 1)]
     ctx.record(evs[0], stream)
     for i in range(steps):
         fn()
         ctx.record(evs[i + 1], stream)
     ctx.synchronize(stream)
     per = [ctx.elapsed_ms(evs[i], evs[i + 1]) for i in range(steps)]
-    total = ctx.elapsed_ms(evs[0], evs[steps])
     for e in evs:
         ctx.destroy_event(e)
-    return np.array(per), total / steps
+    return np.array(per), mean
 
 
 def pct(a, p):
@@ -457,7 +468,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--only-c3", action="store_true", help="time config 3 only (for profiling)")
     ap.add_argument("--rotate", type=int, default=None, help="override TMAC_OPT_ROTATE (tuning)")
