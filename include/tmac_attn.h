@@ -304,6 +304,14 @@ int tmac_attention_prefill(tmac_context* ctx, tmac_stream stream, const float* q
 int tmac_attention_prefill_kv(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
                               const void* k_cache, const void* v_cache, float* out, int n_seq, int n_q,
                               int prefix_len, int64_t seq_stride, int n_head, int n_kv_head, int head_dim);
+/* The same over paged caches (pools of n_pages 16-row pages of kv_dtype; sequence s's row r in
+ * pool page block_table[s][r / 16], as tmac_attention_decode_paged): the tile pack gathers rows
+ * 0..prefix_len + n_q - 1 through the table.  prefix_len + n_q <= 16 * max_pages; an entry
+ * outside the pool is clamped and sets bit 2 of the device error word. */
+int tmac_attention_prefill_paged(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                 const void* k_pages, const void* v_pages, int n_pages, const int32_t* block_table,
+                                 int max_pages, float* out, int n_seq, int n_q, int prefix_len, int n_head,
+                                 int n_kv_head, int head_dim);
 
 /* ---- tuning / introspection ---- */
 enum tmac_option {

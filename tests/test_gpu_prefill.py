@@ -113,6 +113,65 @@ def test_prefill_narrow_caches(ctx, dt, n_seq, n_q, prefix, n_head, n_kv):
                        check=False) == tmac_attn.TMAC_ERR_INVALID_ARG
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16", "q8"])
+def test_prefill_paged(ctx, dt):
+    """tmac_attention_prefill_paged: the rows of 3 sequences scattered over a
+    pool of 16-row pages in random order (sequence 1 sharing sequence 0's
+    first 4 pages) give what the contiguous prefill gives on the same rows."""
+    import tmac_attn
+    n_seq, n_q, prefix, n_head, n_kv, pr = 3, 40, 90, 14, 2, tmac_attn.PAGE_ROWS
+    rows = prefix + n_q
+    kvd = n_kv * HD
+    q, k, v = make(900, n_seq, n_q, prefix, rows, n_head, n_kv)
+    k[1, :4 * pr], v[1, :4 * pr] = k[0, :4 * pr], v[0, :4 * pr]  # the shared prefix pages hold equal rows
+    q = bf16_round(q)
+    if dt == "f32":
+        code, store, widen = tmac_attn.TMAC_KV_F32, (lambda x: x), (lambda b: b)
+    elif dt == "bf16":
+        code = tmac_attn.TMAC_KV_BF16
+        store = lambda x: (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+        widen = lambda b: (b.astype(np.uint32) << 16).view(np.float32)
+    else:
+        code = tmac_attn.TMAC_KV_Q8_0
+        store = lambda x: oracle.q8_kv_rows(x.reshape(-1, HD)).reshape(*x.shape[:-1], n_kv * oracle.Q8_HEAD_BYTES)
+        widen = lambda b: oracle.q8_kv_widen(b).reshape(*b.shape[:-1], kvd)
+    kb, vb = store(k), store(v)
+    max_pages = (rows + pr - 1) // pr
+    n_pages = n_seq * max_pages + 5
+    rng = np.random.default_rng(9)
+    perm = rng.permutation(n_pages)
+    table = np.zeros((n_seq, max_pages), np.int32)
+    kp = np.zeros((n_pages * pr,) + kb.shape[2:], kb.dtype)
+    vp = np.zeros_like(kp)
+    nxt = 0
+    for s in range(n_seq):
+        for j in range(max_pages):
+            if s == 1 and j < 4:
+                table[s, j] = table[0, j]
+                continue
+            table[s, j] = perm[nxt]
+            nxt += 1
+            seg = slice(j * pr, min(rows, (j + 1) * pr))
+            kp[table[s, j] * pr:table[s, j] * pr + seg.stop - seg.start] = kb[s, seg]
+            vp[table[s, j] * pr:table[s, j] * pr + seg.stop - seg.start] = vb[s, seg]
+    dq, dk, dv, dtab = ctx.upload(q), ctx.upload(kp), ctx.upload(vp), ctx.upload(table)
+    out = ctx.empty((n_seq, n_q, n_head * HD))
+    ctx.prefill_paged(dq, dk, dv, n_pages, dtab, max_pages, out, n_seq, n_q, prefix, n_head, n_kv, HD, kv_dtype=code)
+    kw = bf16_round(np.asarray(widen(kb), np.float32).reshape(n_seq, rows, kvd))
+    vw = bf16_round(np.asarray(widen(vb), np.float32).reshape(n_seq, rows, kvd))
+    ref = oracle.prefill(q, kw, vw, n_seq, n_q, prefix, rows, n_head, n_kv, HD, n_threads=8)
+    assert_close(out.numpy(), ref, f"paged prefill {dt}")
+    assert ctx.check_device_error() == 0
+    # an entry outside the pool is clamped (no out-of-bounds read) and reported (bit 2)
+    bad = table.copy()
+    bad[2, 3] = n_pages + 7
+    ctx.prefill_paged(dq, dk, dv, n_pages, ctx.upload(bad), max_pages, out, n_seq, n_q, prefix, n_head, n_kv, HD,
+                      kv_dtype=code)
+    assert ctx.check_device_error() == tmac_attn.TMAC_ERR_DEVICE_FAULT
+    assert ctx.prefill_paged(dq, dk, dv, n_pages, dtab, 2, out, n_seq, n_q, prefix, n_head, n_kv, HD,
+                             kv_dtype=code, check=False) == tmac_attn.TMAC_ERR_INVALID_ARG  # rows > 16 * max_pages
+
+
 def test_prefill_rejects_bad_arguments(ctx):
     import tmac_attn
     d = ctx.empty(16 * 14 * HD)

@@ -75,6 +75,12 @@ struct PrefillArgs {
     uint16_t* packed;        // bf16 tiles [n_seq][n_kv_head][n_tp][K tile, V^T tile] (64 x 64 each)
     int n_tp;                // tiles per (sequence, kv head): ceil(n_rows / 64) rounded up to a stage
     int n_rows;              // prefix_len + n_q: cache rows that are packed
+    // paged caches: k / v are pools of n_pages kPageRows-row pages, sequence s's
+    // row r in pool page block_table[s][r / kPageRows] (seq_stride unused)
+    const int32_t* block_table;
+    int max_pages;
+    int n_pages;
+    int* err;                // bit 2: a block-table entry outside the pool (clamped)
 };
 constexpr int kPrefillQueries = 16;  // queries per workgroup (one MFMA column block)
 constexpr int kPrefillKeys = 64;     // keys per tile

@@ -1126,12 +1126,12 @@ __device__ __forceinline__ float sum4_rows(float v) {
 }
 
 // Pack one 64-row tile of one (sequence, kv head) from a cache of element
-// type T (fp32, bf16, fp16 or Q8_0 head rows): 256 threads, thread t owns row
-// t / 4 and the 8-dim chunks q4 and 4 + q4 (q4 = t % 4) of the K tile and of
-// the V^T tile.  Values are widened exactly to fp32 (load_row) and rounded to
-// bf16 (nearest even; exact for a bf16 cache).  Rows at or past n_rows are
-// written as zeros.
-template <typename T, int KV>
+// type T (fp32, bf16, fp16 or Q8_0 head rows), contiguous or paged: 256
+// threads, thread t owns row t / 4 and the 8-dim chunks q4 and 4 + q4
+// (q4 = t % 4) of the K tile and of the V^T tile.  Values are widened exactly
+// to fp32 (load_row) and rounded to bf16 (nearest even; exact for a bf16
+// cache).  Rows at or past n_rows are written as zeros.
+template <typename T, int KV, bool PAGED>
 __device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
     constexpr int HB = CacheFmt<T>::kHeadBytes, ROWB = KV * HB, DB = CacheFmt<T>::kDimBytes;
     const int tile = blockIdx.x % a.n_tp;
@@ -1139,7 +1139,18 @@ __device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
     const int kv = rest % KV, seq = rest / KV;
     const int tid = threadIdx.x, r = tid >> 2, q4 = tid & 3;
     const int key = tile * kPrefillKeys + r;
-    const size_t row = (size_t)seq * a.seq_stride + (size_t)min(key, a.n_rows - 1);
+    const int kr = min(key, a.n_rows - 1);
+    size_t row;
+    if constexpr (PAGED) {
+        int pg = a.block_table[(size_t)seq * a.max_pages + (kr >> kPageShift)];
+        if (pg < 0 || pg >= a.n_pages) {  // clamped into the pool, reported
+            if (key < a.n_rows && (key & (kPageRows - 1)) == 0 && q4 == 0) atomicOr(a.err, 4);  // once per page
+            pg = min(max(pg, 0), a.n_pages - 1);
+        }
+        row = (size_t)pg * kPageRows + (kr & (kPageRows - 1));
+    } else {
+        row = (size_t)seq * a.seq_stride + (size_t)kr;
+    }
     const char* kh = reinterpret_cast<const char*>(a.k) + row * ROWB + kv * HB;
     const char* vh = reinterpret_cast<const char*>(a.v) + row * ROWB + kv * HB;
     const bool valid = key < a.n_rows;
@@ -1455,19 +1466,18 @@ TMAC_PREFILL_KERNEL(4, 2)
 TMAC_PREFILL_KERNEL(4, 4)
 TMAC_PREFILL_KERNEL(8, 1)
 
-#define TMAC_PREFILL_PACK_KERNEL(KV)                                                                       \
-    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_kv##KV(PrefillArgs a) {            \
-        prefill_pack_body<float, KV>(a);                                                                  \
+#define TMAC_PREFILL_PACK_TYPE(KV, TN, T)                                                                  \
+    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_##TN##kv##KV(PrefillArgs a) {      \
+        prefill_pack_body<T, KV, false>(a);                                                               \
     }                                                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_bf16_kv##KV(PrefillArgs a) {       \
-        prefill_pack_body<__bf16, KV>(a);                                                                 \
-    }                                                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_f16_kv##KV(PrefillArgs a) {        \
-        prefill_pack_body<_Float16, KV>(a);                                                               \
-    }                                                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_q8_kv##KV(PrefillArgs a) {         \
-        prefill_pack_body<q8_0_t, KV>(a);                                                                 \
+    extern "C" __global__ __launch_bounds__(256) void tmac_prefill_pack_p_##TN##kv##KV(PrefillArgs a) {    \
+        prefill_pack_body<T, KV, true>(a);                                                                \
     }
+#define TMAC_PREFILL_PACK_KERNEL(KV)            \
+    TMAC_PREFILL_PACK_TYPE(KV, , float)         \
+    TMAC_PREFILL_PACK_TYPE(KV, bf16_, __bf16)   \
+    TMAC_PREFILL_PACK_TYPE(KV, f16_, _Float16)  \
+    TMAC_PREFILL_PACK_TYPE(KV, q8_, q8_0_t)
 TMAC_PREFILL_PACK_KERNEL(1)
 TMAC_PREFILL_PACK_KERNEL(2)
 TMAC_PREFILL_PACK_KERNEL(4)

@@ -110,7 +110,7 @@ struct tmac_context {
     // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged, layer, paged layer
     std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
-    std::map<int, hipFunction_t> prefill_pack[4];             // prefill tile packing, by cache type and KV
+    std::map<int, hipFunction_t> prefill_pack[2][4];          // prefill tile packing: [paged][cache type], by KV
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
                   k_kq = nullptr, k_cvt_q8 = nullptr;
     float* ws = nullptr;
@@ -543,13 +543,15 @@ int tmac_init(tmac_context** out, int device) {
                     return bail(hip_fail(ctx, e, name));
                 ctx->prefill[{sh[0], sh[1]}] = f;
                 static const char* const pack_type[4] = {"", "bf16_", "f16_", "q8_"};
-                for (int dt = 0; dt < 4; ++dt) {
-                    if (ctx->prefill_pack[dt].count(sh[1])) continue;
-                    std::snprintf(name, sizeof(name), "tmac_prefill_pack_%skv%d", pack_type[dt], sh[1]);
-                    if ((e = get_function(ctx, &f, name)) != hipSuccess)
-                        return bail(hip_fail(ctx, e, name));
-                    ctx->prefill_pack[dt][sh[1]] = f;
-                }
+                for (int pg = 0; pg < 2; ++pg)
+                    for (int dt = 0; dt < 4; ++dt) {
+                        if (ctx->prefill_pack[pg][dt].count(sh[1])) continue;
+                        std::snprintf(name, sizeof(name), "tmac_prefill_pack_%s%skv%d", pg ? "p_" : "", pack_type[dt],
+                                      sh[1]);
+                        if ((e = get_function(ctx, &f, name)) != hipSuccess)
+                            return bail(hip_fail(ctx, e, name));
+                        ctx->prefill_pack[pg][dt][sh[1]] = f;
+                    }
             }
         }
     }
@@ -868,9 +870,12 @@ int tmac_kv_convert(tmac_context* ctx, tmac_stream stream, int kv_dtype, const f
     return launch(ctx, ctx->k_cvt16, (unsigned)((n + 255) / 256), 1, 256, (hipStream_t)stream, &a);
 }
 
+// Chunked prefill over a contiguous cache (block_table null: sequence s at row
+// s * seq_stride) or a paged one (n_pages pages, block_table [n_seq][max_pages]).
 static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const float* q, const void* k_cache,
                         const void* v_cache, float* out, int n_seq, int n_q, int prefix_len, int64_t seq_stride,
-                        int n_head, int n_kv_head, int head_dim) {
+                        int n_head, int n_kv_head, int head_dim, const int32_t* block_table = nullptr,
+                        int max_pages = 0, int n_pages = 0) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if (dt != TMAC_KV_F32 && dt != TMAC_KV_BF16 && dt != TMAC_KV_F16 && dt != TMAC_KV_Q8_0)
@@ -881,8 +886,11 @@ static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const flo
     if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, nullptr, kModeUniform))) return rc;
     if (n_seq < 0 || n_q < 0 || prefix_len < 0 || (int64_t)prefix_len + n_q > INT_MAX)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: need n_seq, n_q, prefix_len >= 0");
-    if (n_seq > 1 && seq_stride < (int64_t)prefix_len + n_q)
+    if (!block_table && n_seq > 1 && seq_stride < (int64_t)prefix_len + n_q)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: seq_stride must cover prefix_len + n_q rows");
+    if (block_table && (n_pages < 1 || max_pages < 1 || (int64_t)prefix_len + n_q > (int64_t)max_pages * kPageRows))
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_paged: need n_pages, max_pages >= 1 and "
+                                               "prefix_len + n_q <= 16 * max_pages");
     if ((int64_t)((n_q + kPrefillQueries - 1) / kPrefillQueries) * n_kv_head * n_seq > INT_MAX)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: too many (query block, kv head, sequence) units");
     if (n_seq == 0 || n_q == 0) return TMAC_OK;
@@ -900,9 +908,10 @@ static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const flo
     const size_t pack_bytes = (size_t)pack_blocks * kPrefillTileElems * sizeof(uint16_t);
     if ((rc = ensure_workspace(ctx, (hipStream_t)stream, pack_bytes / sizeof(float)))) return rc;
     PrefillArgs a{q, static_cast<const float*>(k_cache), static_cast<const float*>(v_cache), out, seq_stride, n_q,
-                  prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(ctx->ws), n_tp, n_rows};
-    if ((rc = launch(ctx, ctx->prefill_pack[dt].at(n_kv_head), (unsigned)pack_blocks, 1, 256, (hipStream_t)stream,
-                     &a)))
+                  prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(ctx->ws), n_tp, n_rows,
+                  block_table, max_pages, n_pages, ctx->err};
+    if ((rc = launch(ctx, ctx->prefill_pack[block_table ? 1 : 0][dt].at(n_kv_head), (unsigned)pack_blocks, 1, 256,
+                     (hipStream_t)stream, &a)))
         return rc;
     return launch(ctx, it->second, (unsigned)((int64_t)n_qblk * n_kv_head * n_seq), 1, kPrefillWaves * 64,
                   (hipStream_t)stream, &a);
@@ -920,6 +929,18 @@ int tmac_attention_prefill_kv(tmac_context* ctx, tmac_stream stream, int kv_dtyp
                               int prefix_len, int64_t seq_stride, int n_head, int n_kv_head, int head_dim) {
     return prefill_impl(ctx, stream, kv_dtype, q, k_cache, v_cache, out, n_seq, n_q, prefix_len, seq_stride,
                         n_head, n_kv_head, head_dim);
+}
+
+int tmac_attention_prefill_paged(tmac_context* ctx, tmac_stream stream, int kv_dtype, const float* q,
+                                 const void* k_pages, const void* v_pages, int n_pages, const int32_t* block_table,
+                                 int max_pages, float* out, int n_seq, int n_q, int prefix_len, int n_head,
+                                 int n_kv_head, int head_dim) {
+    if (!block_table) {
+        const int rc = check_ctx(ctx);
+        return rc ? rc : fail(ctx, TMAC_ERR_NULL_POINTER, "prefill_paged: null block table");
+    }
+    return prefill_impl(ctx, stream, kv_dtype, q, k_pages, v_pages, out, n_seq, n_q, prefix_len, 0, n_head,
+                        n_kv_head, head_dim, block_table, max_pages, n_pages);
 }
 
 int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add) {

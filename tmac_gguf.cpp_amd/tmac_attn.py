@@ -98,6 +98,7 @@ SIGNATURES = {
     "tmac_attention_decode_ragged": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
     "tmac_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_attention_prefill_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
+    "tmac_attention_prefill_paged": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i]),
     "tmac_set_option": (_i, [_vp, _i, _i64]),
     "tmac_query_split": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "tmac_check_device_error": (_i, [_vp]),
@@ -499,6 +500,15 @@ class Context:
                                                     n_seq, n_q, prefix_len, seq_stride, n_head, n_kv_head, head_dim)
         if check:
             self._check(rc, "prefill")
+        return rc
+
+    def prefill_paged(self, q, k_pages, v_pages, n_pages, block_table, max_pages, out, n_seq, n_q, prefix_len,
+                      n_head, n_kv_head, head_dim, stream=None, check=True, kv_dtype=TMAC_KV_F32) -> int:
+        rc = self.lib.tmac_attention_prefill_paged(self.handle, stream, kv_dtype, _p(q), _p(k_pages), _p(v_pages),
+                                                   n_pages, _p(block_table), max_pages, _p(out), n_seq, n_q,
+                                                   prefix_len, n_head, n_kv_head, head_dim)
+        if check:
+            self._check(rc, "prefill_paged")
         return rc
 
     # -- step capture ----------------------------------------------------------
