@@ -91,6 +91,12 @@ int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, con
  * context builds on the host with the platform libm (tmac_rope_prepare). */
 int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads, int head_dim,
                  int pos, float base);
+/* rope_op over n_rows rows (row r at data + r * row_stride floats, n_heads heads each) at positions
+ * first_pos + r: the RoPE of a prompt chunk before its rows are written to the cache.  Row r is
+ * bit-identical to tmac_rope_op at position first_pos + r.  No counterpart in the reference, which
+ * feeds a prompt one token at a time (tmac_gguf.cpp:1621-1658). */
+int tmac_rope_rows(tmac_context* ctx, tmac_stream stream, float* data, int n_rows, int64_t row_stride, int n_heads,
+                   int head_dim, int first_pos, float base);
 
 /* elem_op, metal_backend.hpp:354-379 (kernel_elem.metal:14-21), i < dim:
  *   op 2, cache write  data[i] = aux[i]   (tmac_gguf.cpp:1090-1091, 1564-1565)

@@ -72,6 +72,22 @@ def test_rope_op_bit_exact(ctx, pos):
     np.testing.assert_array_equal(dk.numpy(), rk)
 
 
+@pytest.mark.parametrize("n_heads", [NH, NKV])
+def test_rope_rows_bit_exact(ctx, n_heads):
+    """tmac_rope_rows: 37 rows (padded stride) at positions 1000.. equal
+    rope_op / the oracle row by row, bit for bit; the padding is untouched."""
+    n_rows, first, stride = 37, 1000, n_heads * HD + 32
+    x = oracle.normal(25 + n_heads, (n_rows, stride))
+    d = ctx.upload(x)
+    ctx.rope_rows(d, n_rows, stride, n_heads, HD, first, 1e6)
+    got = d.numpy()
+    for r in range(n_rows):
+        np.testing.assert_array_equal(got[r, :n_heads * HD], oracle.rope_heads(x[r, :n_heads * HD], n_heads, HD,
+                                                                               first + r, 1e6))
+    np.testing.assert_array_equal(got[:, n_heads * HD:], x[:, n_heads * HD:])
+    assert ctx.check_device_error() == 0
+
+
 def test_elem_op_cache_write_bit_exact(ctx):
     cache = oracle.normal(30, (256, KVD))
     src = oracle.normal(31, KVD)

@@ -89,13 +89,15 @@ constexpr int kPrefillStageTiles = 4;           // tiles per LDS stage (two per 
 constexpr int kPrefillWaves = 8;     // waves per workgroup: 4 head pairs x 2 stage halves
 
 struct RopeArgs {
-    float* x;                // [n_heads][64], rotated in place
+    float* x;                // n_rows rows of [n_heads][64], rotated in place; row r at x + r * row_stride
     const float2* rope_cs;   // [rope_rows][32]
-    const int* pos_dev;
+    const int* pos_dev;      // position of row 0 (device; null: pos_host); row r sits at position + r
     int pos_host;
     int n_heads;
     int rope_rows;
     int* err;
+    int n_rows;
+    int64_t row_stride;      // floats between rows
 };
 
 struct CopyArgs {

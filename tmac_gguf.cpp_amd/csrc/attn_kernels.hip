@@ -2206,16 +2206,18 @@ extern "C" __global__ __launch_bounds__(kQkvWaves * 64) void tmac_qkv(QkvArgs a)
 // RoPE in place, one lane per (head, pair): tmac_gguf.cpp:992-1003 for one
 // tensor, i.e. what rope_op (metal_backend.hpp:381) dispatches.
 extern "C" __global__ __launch_bounds__(256) void tmac_rope(RopeArgs a) {
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_row = a.n_heads * (kHeadDim / 2);
+    const int row = gid / per_row, rem = gid - row * per_row;
+    if (row >= a.n_rows) return;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos_host) + row;
     if (pos < 0 || pos >= a.rope_rows) {
-        if (gid == 0) atomicOr(a.err, 1);
+        if (rem == 0) atomicOr(a.err, 1);
         return;
     }
-    const int head = gid >> 5, pair = gid & 31;
-    if (head >= a.n_heads) return;
+    const int head = rem >> 5, pair = rem & 31;
     const float2 t = a.rope_cs[(size_t)pos * (kHeadDim / 2) + pair];
-    float2* p = reinterpret_cast<float2*>(a.x + head * kHeadDim) + pair;
+    float2* p = reinterpret_cast<float2*>(a.x + (size_t)row * a.row_stride + head * kHeadDim) + pair;
     float2 x = *p;
     rotate_pair(x.x, x.y, t.x, t.y);
     *p = x;

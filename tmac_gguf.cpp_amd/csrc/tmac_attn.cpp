@@ -976,8 +976,30 @@ int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads
     if ((rc = set_device(ctx))) return rc;
     const RopeTable* rt = nullptr;
     if ((rc = rope_table(ctx, (hipStream_t)stream, head_dim, base, pos + 1, &rt))) return rc;
-    RopeArgs a{data, rt->dev, nullptr, pos, n_heads, rt->rows, ctx->err};
+    RopeArgs a{data, rt->dev, nullptr, pos, n_heads, rt->rows, ctx->err, 1, 0};
     const int threads = n_heads * (kHeadDim / 2);
+    return launch(ctx, ctx->k_rope, (unsigned)((threads + 255) / 256), 1, 256, (hipStream_t)stream, &a);
+}
+
+int tmac_rope_rows(tmac_context* ctx, tmac_stream stream, float* data, int n_rows, int64_t row_stride, int n_heads,
+                   int head_dim, int first_pos, float base) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!data) return fail(ctx, TMAC_ERR_NULL_POINTER, "rope_rows: null data");
+    if (!aligned16(data) || row_stride % 4 != 0)
+        return fail(ctx, TMAC_ERR_MISALIGNED, "rope_rows: data and rows must be 16-byte aligned");
+    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope_rows: head_dim must be 64");
+    if (n_rows < 0 || n_heads < 0 || first_pos < 0 || (int64_t)first_pos + n_rows > INT_MAX ||
+        (n_rows > 1 && row_stride < (int64_t)n_heads * kHeadDim) ||
+        (int64_t)n_rows * n_heads * (kHeadDim / 2) > INT_MAX)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_rows: bad n_rows / row_stride / n_heads / first_pos");
+    if (!(base > 0.f) || !std::isfinite(base)) return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_rows: bad base");
+    if (n_rows == 0 || n_heads == 0) return TMAC_OK;
+    if ((rc = set_device(ctx))) return rc;
+    const RopeTable* rt = nullptr;
+    if ((rc = rope_table(ctx, (hipStream_t)stream, head_dim, base, first_pos + n_rows, &rt))) return rc;
+    RopeArgs a{data, rt->dev, nullptr, first_pos, n_heads, rt->rows, ctx->err, n_rows, row_stride};
+    const int64_t threads = (int64_t)n_rows * n_heads * (kHeadDim / 2);
     return launch(ctx, ctx->k_rope, (unsigned)((threads + 255) / 256), 1, 256, (hipStream_t)stream, &a);
 }
 

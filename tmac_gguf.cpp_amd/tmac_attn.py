@@ -99,6 +99,7 @@ SIGNATURES = {
     "tmac_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_attention_prefill_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_attention_prefill_paged": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i]),
+    "tmac_rope_rows": (_i, [_vp, _vp, _vp, _i, _i64, _i, _i, _i, _f]),
     "tmac_set_option": (_i, [_vp, _i, _i64]),
     "tmac_query_split": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "tmac_check_device_error": (_i, [_vp]),
@@ -353,6 +354,14 @@ class Context:
                                         n_head, n_kv_head, head_dim, past_len)
         if check:
             self._check(rc, "attention_op")
+        return rc
+
+    def rope_rows(self, data, n_rows, row_stride, n_heads, head_dim, first_pos, base=1e6, stream=None,
+                  check=True) -> int:
+        rc = self.lib.tmac_rope_rows(self.handle, stream, _p(data), n_rows, row_stride, n_heads, head_dim, first_pos,
+                                     base)
+        if check:
+            self._check(rc, "rope_rows")
         return rc
 
     def rope_op(self, data, n_heads, head_dim, pos, base=1e6, stream=None, check=True) -> int:
