@@ -172,6 +172,63 @@ def test_prefill_paged(ctx, dt):
                              kv_dtype=code, check=False) == tmac_attn.TMAC_ERR_INVALID_ARG  # rows > 16 * max_pages
 
 
+@pytest.mark.parametrize("dt", ["f32", "q8"])
+def test_chunked_prompt_rope_rows_write_prefill(ctx, dt):
+    """A 300-token prompt fed in 64-token chunks the way a caller would:
+    tmac_rope_rows rotates the chunk's q and k rows, the rotated k and v rows
+    go into the cache (a device copy for fp32, tmac_kv_convert for Q8_0), and
+    the chunk's prefill attends rows 0..its position.  The cache rows equal
+    the oracle's RoPE (tmac_gguf.cpp:990-1016) and Q8_0 rule bit for bit; the
+    outputs equal the oracle's attention on the bf16-rounded rotated rows."""
+    import ctypes
+    import tmac_attn
+    nh, nkv, n_tok, chunk = 14, 2, 300, 64
+    kvd = nkv * HD
+    cap = 320
+    q_all = oracle.normal(950, (n_tok, nh * HD))
+    k_all = oracle.normal(951, (n_tok, kvd))
+    v_all = oracle.normal(952, (n_tok, kvd))
+    q8 = dt == "q8"
+    rb = nkv * oracle.Q8_HEAD_BYTES if q8 else kvd
+    dk = ctx.upload(np.zeros((cap, rb), np.uint8 if q8 else np.float32))
+    dv = ctx.upload(np.zeros((cap, rb), np.uint8 if q8 else np.float32))
+    ref_k = np.zeros((cap, kvd), np.float32)  # rotated rows as the cache holds them (widened)
+    ref_v = np.zeros((cap, kvd), np.float32)
+    ref_k_bytes = np.zeros((cap, rb), np.uint8 if q8 else np.float32)
+    for c0 in range(0, n_tok, chunk):
+        n = min(chunk, n_tok - c0)
+        dq, dkc, dvc = ctx.upload(q_all[c0:c0 + n]), ctx.upload(k_all[c0:c0 + n]), ctx.upload(v_all[c0:c0 + n])
+        ctx.rope_rows(dq, n, nh * HD, nh, HD, c0, 1e6)
+        ctx.rope_rows(dkc, n, kvd, nkv, HD, c0, 1e6)
+        if q8:
+            ctx.kv_convert(tmac_attn.TMAC_KV_Q8_0, dkc, dk.at(c0 * rb), n * kvd)
+            ctx.kv_convert(tmac_attn.TMAC_KV_Q8_0, dvc, dv.at(c0 * rb), n * kvd)
+        else:
+            for src, dst in ((dkc, dk), (dvc, dv)):
+                rc = ctx.lib.tmac_memcpy_d2d(ctx.handle, None, ctypes.c_void_p(dst.at(c0 * kvd)),
+                                             ctypes.c_void_p(src.ptr), n * kvd * 4)
+                assert rc == 0
+        out = ctx.empty((1, n, nh * HD))
+        ctx.prefill(dq, dk, dv, out, 1, n, c0, cap, nh, nkv, HD, kv_dtype=tmac_attn.TMAC_KV_Q8_0 if q8 else 0)
+        q_rot = np.empty((n, nh * HD), np.float32)
+        for i in range(n):
+            qr, kr = oracle.rope(q_all[c0 + i], k_all[c0 + i], nh, nkv, HD, c0 + i, 1e6)
+            q_rot[i] = qr
+            if q8:
+                ref_k_bytes[c0 + i] = oracle.q8_kv_rows(kr.reshape(-1, HD)).reshape(-1)
+                ref_k[c0 + i] = oracle.q8_kv_widen(ref_k_bytes[c0 + i]).reshape(-1)
+                ref_v[c0 + i] = oracle.q8_kv_widen(oracle.q8_kv_rows(v_all[c0 + i].reshape(-1, HD))).reshape(-1)
+            else:
+                ref_k_bytes[c0 + i] = kr
+                ref_k[c0 + i], ref_v[c0 + i] = kr, v_all[c0 + i]
+        np.testing.assert_array_equal(dq.numpy(), q_rot)  # the chunk RoPE, bit for bit
+        ref = oracle.prefill(bf16_round(q_rot)[None], bf16_round(ref_k)[None], bf16_round(ref_v)[None], 1, n, c0,
+                             cap, nh, nkv, HD, n_threads=8)
+        assert_close(out.numpy(), ref, f"chunk at {c0} ({dt})")
+    np.testing.assert_array_equal(dk.numpy()[:n_tok], ref_k_bytes[:n_tok])
+    assert ctx.check_device_error() == 0
+
+
 def test_prefill_rejects_bad_arguments(ctx):
     import tmac_attn
     d = ctx.empty(16 * 14 * HD)
