@@ -586,6 +586,8 @@ def main():
         "pct_of_peak": round(gbs / HBM_PEAK_GBS * 100, 2),
         "us_per_call": round(c3["mean_ms"] * 1e3, 2),
         "us_per_call_median": round(c3["median_ms"] * 1e3, 2),
+        "us_per_call_p10": round(c3["p10_ms"] * 1e3, 2),
+        "us_per_call_p90": round(c3["p90_ms"] * 1e3, 2),
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 2),
