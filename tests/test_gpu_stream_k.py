@@ -1,0 +1,145 @@
+"""GPU parity of the stream-K ragged decode (fp32 caches; one of the two
+schedules of tmac_attention_decode_ragged, forced here with TMAC_OPT_STREAM_K=2).
+
+The batch's rows, each sequence padded to 16 rows, are cut on the device into
+equal ranges, one workgroup each; a sequence may span several ranges and a
+range several sequences.  The workgroup count is swept from 1 (one workgroup
+takes the whole batch) to more than the rows allow (64-row ranges, a 5,000-row
+sequence over 79 of them), and the row-count hint (unused by this schedule)
+from none to far too low.  Every result is checked against the
+oracle (tmac_gguf.cpp:1093-1128 per sequence) with the attention tolerance
+2e-5 + 1e-4 |ref|, and empty and over-long sequences keep the entry point's
+contract (zeros; NaN and error bit 1).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import tmac_attn
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+NH, NKV, HD = 14, 2, 64
+KVD = NKV * HD
+
+
+@pytest.fixture(autouse=True)
+def stream_k(ctx):
+    ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 2)
+    yield
+    ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 1)
+
+
+def ragged_batch(ctx, seed, lens):
+    lens = np.asarray(lens, np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens[:-1], dtype=np.int64)]).astype(np.int64)
+    total = int(lens.sum())
+    k, v = oracle.normal(seed, (max(total, 1), KVD)), oracle.normal(seed + 1, (max(total, 1), KVD))
+    q = oracle.normal(seed + 2, (lens.size, NH * HD))
+    return lens, offs, total, k, v, q
+
+
+def reference(q, k, v, offs, lens):
+    ref = np.zeros((lens.size, NH * HD), np.float32)
+    nz = lens > 0
+    ref[nz] = oracle.attention_ragged(q[nz], k, v, offs[nz], lens[nz], NH, NKV, HD, n_threads=8)
+    return ref
+
+
+@pytest.mark.parametrize("groups", [1, 3, 37, 0, 600])
+def test_stream_k_matches_oracle(ctx, groups):
+    lens, offs, total, k, v, q = ragged_batch(
+        ctx, 4100, [0, 1, 15, 16, 17, 63, 64, 65, 300, 2048, 5000, 0, 33, 7, 4097, 1])
+    ref = reference(q, k, v, offs, lens)
+    dq, dk, dv, doff, dlen = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.upload(offs), ctx.upload(lens)
+    dout = ctx.empty((lens.size, NH * HD))
+    ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, groups)
+    try:
+        for hint in (0, 1, total // 3, total):
+            dout.fill_bytes(0xFF)
+            ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, lens.size, NH, NKV, HD, int(lens.max()),
+                              total_rows=hint)
+            assert_close(dout.numpy(), ref, f"stream-K groups={groups} hint={hint}")
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, 0)
+    assert ctx.check_device_error() == 0
+
+
+def test_stream_k_equals_unit_grid(ctx):
+    """Both schedules of the fp32 ragged decode on 200 sequences of 1..3000 rows
+    agree with the oracle (the merge order differs, so not bit for bit)."""
+    rng = np.random.default_rng(41)
+    lens, offs, total, k, v, q = ragged_batch(ctx, 4200, rng.integers(1, 3001, 200))
+    ref = reference(q, k, v, offs, lens)
+    dq, dk, dv, doff, dlen = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.upload(offs), ctx.upload(lens)
+    dout = ctx.empty((lens.size, NH * HD))
+    try:
+        for sk in (2, 0):
+            ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, sk)
+            dout.fill_bytes(0xFF)
+            ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, lens.size, NH, NKV, HD, int(lens.max()),
+                              total_rows=total)
+            assert_close(dout.numpy(), ref, f"stream_k={sk}")
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 2)
+    assert ctx.check_device_error() == 0
+
+
+def test_stream_k_over_long_sequence(ctx):
+    """A length above max_len gives a NaN output and error bit 1; the other
+    sequences of the batch, before and after it in the row space, are exact."""
+    lens, offs, total, k, v, q = ragged_batch(ctx, 4300, [700, 900, 1200, 5])
+    ref = reference(q, k, v, offs, lens)
+    dq, dk, dv, doff, dlen = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.upload(offs), ctx.upload(lens)
+    dout = ctx.empty((lens.size, NH * HD))
+    ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, 9)
+    try:
+        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, lens.size, NH, NKV, HD, 1000, total_rows=total)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, 0)
+    got = dout.numpy()
+    assert np.all(np.isnan(got[2]))
+    keep = np.array([0, 1, 3])
+    assert_close(got[keep], ref[keep], "sequences beside the over-long one")
+    assert ctx.check_device_error() == tmac_attn.TMAC_ERR_DEVICE_FAULT
+    assert ctx.check_device_error() == 0
+
+
+def test_stream_k_graph_replay_new_lengths(ctx):
+    """A captured stream-K decode reads the lengths on the device: replays after
+    the lengths (and queries) change, within the captured max_len and row-count
+    hint, are exact, with eager calls of other shapes between the replays."""
+    max_len, n_seq, cap = 4000, 24, 24 * 4000
+    k, v = oracle.normal(4400, (cap, KVD)), oracle.normal(4401, (cap, KVD))
+    offs = np.arange(n_seq, dtype=np.int64) * max_len
+    dk, dv, doff = ctx.upload(k), ctx.upload(v), ctx.upload(offs)
+    dq, dlen, dout = ctx.empty((n_seq, NH * HD)), ctx.empty(n_seq, np.int32), ctx.empty((n_seq, NH * HD))
+    s = ctx.stream()
+    rng = np.random.default_rng(44)
+    hint = n_seq * max_len // 2
+    try:
+        dlen.copy_from(np.full(n_seq, 1, np.int32))
+        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, n_seq, NH, NKV, HD, max_len, total_rows=hint, stream=s)
+        ctx.synchronize(s)
+        ctx.step_begin(s)
+        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, n_seq, NH, NKV, HD, max_len, total_rows=hint, stream=s)
+        g = ctx.step_end(s)
+        try:
+            for rep in range(4):
+                lens = rng.integers(0, max_len + 1, n_seq).astype(np.int32)
+                q = oracle.normal(4500 + rep, (n_seq, NH * HD))
+                dq.copy_from(q)
+                dlen.copy_from(lens)
+                ctx.graph_launch(g, s)
+                ctx.synchronize(s)
+                assert_close(dout.numpy(), reference(q, k, v, offs, lens), f"replay {rep}")
+                e_lens = np.full(3, 2500, np.int32)  # an eager call of another shape in between
+                ctx.decode_ragged(dq, dk, dv, doff, ctx.upload(e_lens), dout, 3, NH, NKV, HD, 2500, stream=s)
+                ctx.synchronize(s)
+                assert_close(dout.numpy()[:3], reference(q[:3], k, v, offs[:3], e_lens), f"eager {rep}")
+        finally:
+            ctx.graph_destroy(g)
+    finally:
+        ctx.destroy_stream(s)
+    assert ctx.check_device_error() == 0

@@ -58,6 +58,8 @@ struct DecodeArgs {
     const int32_t* positions;    // paged layer mode: [n_seq] position of each sequence's new token
     int max_pages;
     int n_pages;                 // pages in each pool
+    // stream-K ragged decode: per sequence (first workspace slot, slots used)
+    int32_t* seg_meta;
 };
 
 // Chunked causal prefill: query i of sequence s sits at absolute position

@@ -750,6 +750,170 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     finish<GW, KVS, NW>(st, lane, wave, direct, out_heads, ws_split);
 }
 
+// Rows a ragged sequence of length `len` occupies in the stream-K row space:
+// rounded up to kPageRows, and none for an empty sequence or one longer than
+// the launch's max_len (its output is written by the combine).
+__device__ __forceinline__ int64_t sk_rows(int len, int max_len) {
+    return (len > 0 && len <= max_len) ? (((int64_t)len + kPageRows - 1) & ~(int64_t)(kPageRows - 1)) : 0;
+}
+
+// Stream-K ragged decode.  The batch's sequences, each padded to a multiple of
+// kPageRows rows, are laid end to end in one row space of R rows, cut into
+// gridDim.x equal ranges of S = max(ceil(R / gridDim.x) rounded up to
+// kPageRows, kSkMinRows) rows; workgroup u attends the part of every sequence
+// that falls in [u*S, (u+1)*S).  Every workgroup thus streams the same number
+// of bytes whatever the length mix, and equal lengths that divide evenly give
+// one sequence per workgroup.
+// The segment (sequence s, workgroup u) writes its partial to slot u + s of
+// the workspace.  Slots are unique: when u - 1 reaches sequence s + 1, u
+// starts after s.  Sequence s owns the consecutive slots uf + s .. ul + s
+// (uf, ul: the workgroups holding its first and last rows), and workgroup uf
+// records (uf + s, ul - uf + 1) in seg_meta[s] for the combine.  A sequence
+// inside one workgroup's range is written to the output directly.
+constexpr int kSkMinRows = 64;
+template <typename T, int G, int KV, int NW, int DEPTH>
+__device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
+    constexpr int HB = CacheFmt<T>::kHeadBytes;
+    constexpr int ROWB = KV * HB;
+    constexpr int NH = KV * G;
+    constexpr int NT = NW * 64;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int u = blockIdx.x;
+    __shared__ int64_t s_wsum[NW];
+    __shared__ int64_t s_hit[2];  // (sequence, its first row)
+
+    // 1. R: every thread sums the padded lengths of sequences t, t + NT, ...;
+    //    the first kKeep rounds' values stay in registers for the search below
+    //    (their loads are all issued before any is used).
+    constexpr int kKeep = 4;
+    int64_t kept[kKeep];
+#pragma unroll
+    for (int r = 0; r < kKeep; ++r) {
+        const int sq = r * NT + (int)threadIdx.x;
+        kept[r] = sq < a.n_seq ? sk_rows(a.lengths[sq], a.capacity) : 0;
+    }
+    int64_t mine = 0;
+#pragma unroll
+    for (int r = 0; r < kKeep; ++r) mine += kept[r];
+    for (int sq = (int)threadIdx.x + kKeep * NT; sq < a.n_seq; sq += NT) mine += sk_rows(a.lengths[sq], a.capacity);
+#pragma unroll
+    for (int mask = 1; mask < 64; mask <<= 1) mine += __shfl_xor(mine, mask);
+    if (lane == 0) s_wsum[wave] = mine;
+    if (threadIdx.x == 0) s_hit[0] = -1;
+    __syncthreads();
+    int64_t R = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) R += s_wsum[w];
+    int64_t S = (R + gridDim.x - 1) / gridDim.x;
+    S = max((S + kPageRows - 1) & ~(int64_t)(kPageRows - 1), (int64_t)kSkMinRows);
+    const int64_t lo = (int64_t)u * S, hi = lo + S;
+    const int last_u = (int)min((R - 1) / S, (int64_t)gridDim.x - 1);  // last workgroup with rows
+    if (lo >= R) return;  // uniform: every thread has the same R
+    __syncthreads();      // s_wsum is reused below
+
+    // 2. The sequence holding row lo, and its first row: a workgroup-wide
+    //    inclusive scan of the padded lengths, NT sequences per round, until a
+    //    round contains lo.
+    int64_t base = 0;
+    for (int c0 = 0, r = 0; c0 < a.n_seq; c0 += NT, ++r) {
+        const int sq = c0 + (int)threadIdx.x;
+        int64_t rows = 0;
+        if (r < kKeep) {
+#pragma unroll
+            for (int j = 0; j < kKeep; ++j) rows = j == r ? kept[j] : rows;
+        } else {
+            rows = sq < a.n_seq ? sk_rows(a.lengths[sq], a.capacity) : 0;
+        }
+        int64_t incl = rows;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int64_t t = __shfl_up(incl, off);
+            if (lane >= off) incl += t;
+        }
+        if (lane == 63) s_wsum[wave] = incl;
+        __syncthreads();
+        int64_t before = base, total = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int64_t x = s_wsum[w];
+            before += w < wave ? x : 0;
+            total += x;
+        }
+        const int64_t first = before + incl - rows;
+        if (rows > 0 && first <= lo && lo < first + rows) {
+            s_hit[0] = sq;
+            s_hit[1] = first;
+        }
+        __syncthreads();  // also orders this round's s_wsum reads before the next round's writes
+        if (s_hit[0] >= 0) break;
+        base += total;
+    }
+
+    // 3. One segment per sequence overlapping [lo, hi).  The next segment's
+    //    query is loaded before this one's merge, so its latency overlaps it.
+    const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
+    const int lane_row = slot / KV;
+    const int kvh = slot % KV;
+    const int lane_col = kvh * HB + 4 * c * CacheFmt<T>::kDimBytes;
+    const int lane_off = lane_row * ROWB + lane_col;
+    // Advances (s, P) to the first sequence from s on with rows in [lo, hi);
+    // false when there is none.  len: its length.
+    auto seek = [&](int& s, int64_t& P, int& len) -> bool {
+        for (; s < a.n_seq && P < hi; ++s) {
+            s = __builtin_amdgcn_readfirstlane(s);
+            len = __builtin_amdgcn_readfirstlane(a.lengths[s]);
+            const int64_t rows = sk_rows(len, a.capacity);
+            if (rows > 0 && lo - P < (int64_t)len) return true;  // lo - P < len: a row of s lies in [lo, hi)
+            P += rows;
+        }
+        return false;
+    };
+    auto load_q = [&](float (&q)[G][kDimsPerLane], int s) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) load8(q[g], a.q + ((size_t)s * NH + kvh * G + g) * kHeadDim + 4 * c);
+    };
+    int s = (int)s_hit[0], len = 0;
+    int64_t P = s_hit[1];
+    if (!seek(s, P, len)) return;
+    float q[G][kDimsPerLane];
+    load_q(q, s);
+    while (true) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int t = 0; t < kDimsPerLane; ++t) q[g][t] *= a.qscale;
+        const int64_t r0 = max(lo - P, (int64_t)0), r1 = min(hi - P, (int64_t)len);
+        State<G> st;
+        state_init(st);
+        const size_t row0 = (size_t)a.offsets[s] + (size_t)r0;
+        const char* kc = reinterpret_cast<const char*>(a.k) + row0 * ROWB;
+        const char* vc = reinterpret_cast<const char*>(a.v) + row0 * ROWB;
+        const PageMap pm{nullptr, 0, 0};
+        unsigned bad = 0;
+        attend_rows<T, G, KV, ROWB, NW, DEPTH, false>(kc, vc, (int)(r1 - r0), wave, lane_off, lane_row, lane_col, c,
+                                                     q, st, u * a.rot_mul, a.blocked != 0, pm, bad);
+        const int uf = (int)min(P / S, (int64_t)last_u);
+        const int ul = (int)min((P + len - 1) / S, (int64_t)last_u);
+        int s2 = s + 1, len2 = 0;
+        int64_t P2 = P + sk_rows(len, a.capacity);
+        const bool more = seek(s2, P2, len2);
+        if (more) load_q(q, s2);
+        if (u == uf && threadIdx.x == 0) {
+            a.seg_meta[2 * s] = uf + s;
+            a.seg_meta[2 * s + 1] = ul - uf + 1;
+        }
+        const bool direct = uf == ul;
+        float* ws_slot = direct ? nullptr : a.ws + (size_t)(u + s) * NH * kPartialStride;
+        finish<G, KV, NW>(st, lane, wave, direct, a.out + (size_t)s * NH * kHeadDim, ws_slot);
+        if (!more) break;
+        __syncthreads();  // the next segment's finish rewrites the LDS this one merged from
+        s = s2;
+        P = P2;
+        len = len2;
+    }
+}
+
 // Head decode for short contexts: workgroup = (query head, sequence), one
 // split, NW waves; a step is 8 rows of this head's kv head (256-byte halves of
 // the cache rows).  Everything that does not depend on the attended length --
@@ -906,18 +1070,11 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
 // and the l-weighted sum are wave reductions, and split j's weight reaches
 // every lane by readlane, so a chunk costs one memory latency; later chunks
 // (more than 32 splits) rescale by the running max.
-template <int G, int KV, int MODE>
-__device__ __forceinline__ void combine_body(const DecodeArgs& a) {
-    constexpr int NH = KV * G, B = 32;
-    constexpr size_t SP = (size_t)NH * kPartialStride;  // floats between splits
-    const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
-    int n_pos, pos;
-    size_t base;
-    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) return;
-    if (n_pos <= 0) return;
-    const int n_act = (n_pos + a.split_len - 1) / a.split_len;
-    if (n_act <= 1 || n_act > a.n_splits) return;
-    const float* ws = a.ws + (size_t)seq * a.n_splits * SP + (size_t)h * kPartialStride;
+// Merged value of output dim d over n_act partials, the first at ws (the
+// head's partial in that slot) and the rest SP floats apart.
+template <int SP>
+__device__ __forceinline__ float merge_splits(const float* __restrict__ ws, int n_act, int d) {
+    constexpr int B = 32;
     float M = kNegInf, L = 0.f, A = 0.f;
     for (int c0 = 0; c0 < n_act; c0 += B) {
         const int n = min(B, n_act - c0);
@@ -947,7 +1104,46 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
         L = fmaf(L, sc, lw);
         M = nm;
     }
-    a.out[((size_t)seq * NH + h) * kHeadDim + d] = A / L;
+    return A / L;
+}
+
+template <int G, int KV, int MODE>
+__device__ __forceinline__ void combine_body(const DecodeArgs& a) {
+    constexpr int NH = KV * G;
+    constexpr int SP = NH * kPartialStride;  // floats between splits
+    const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+    int n_pos, pos;
+    size_t base;
+    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) return;
+    if (n_pos <= 0) return;
+    const int n_act = (n_pos + a.split_len - 1) / a.split_len;
+    if (n_act <= 1 || n_act > a.n_splits) return;
+    const float* ws = a.ws + (size_t)seq * a.n_splits * SP + (size_t)h * kPartialStride;
+    a.out[((size_t)seq * NH + h) * kHeadDim + d] = merge_splits<SP>(ws, n_act, d);
+}
+
+// Combine of the stream-K ragged decode: one wave per (head, sequence).  It
+// also writes the outputs of the sequences the decode kernel skips: zeros for
+// an empty sequence, NaN (and error bit 1) for one longer than max_len.
+template <int G, int KV>
+__device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
+    constexpr int NH = KV * G;
+    constexpr int SP = NH * kPartialStride;
+    const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+    const int len = a.lengths[seq];
+    float* o = a.out + ((size_t)seq * NH + h) * kHeadDim + d;
+    if (len <= 0) {
+        *o = 0.f;
+        return;
+    }
+    if (len > a.capacity) {
+        *o = __builtin_nanf("");
+        if (h == 0 && d == 0) atomicOr(a.err, 2);
+        return;
+    }
+    const int first = a.seg_meta[2 * seq], n_act = a.seg_meta[2 * seq + 1];
+    if (n_act <= 1) return;  // written by the decode kernel
+    *o = merge_splits<SP>(a.ws + (size_t)first * SP + (size_t)h * kPartialStride, n_act, d);
 }
 
 }  // namespace
@@ -972,6 +1168,15 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(64) void tmac_##M##_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, MODE>(a);                                                              \
+    }
+
+// Stream-K ragged decode (fp32 caches) and its combine.
+#define TMAC_SK_KERNELS(G, KV)                                                                     \
+    extern "C" __global__ __launch_bounds__(256) void tmac_decode_sk_g##G##_kv##KV(DecodeArgs a) {  \
+        decode_sk_body<float, G, KV, 4, kPrefetchDepth>(a);                                        \
+    }                                                                                              \
+    extern "C" __global__ __launch_bounds__(64) void tmac_decode_sk_combine_g##G##_kv##KV(DecodeArgs a) { \
+        combine_sk_body<G, KV>(a);                                                                 \
     }
 
 // Narrow caches (bf16, fp16, Q8_0): the default group (8 waves) and head
@@ -1001,7 +1206,8 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
 #define TMAC_DECODE_F32(G, KV)                       \
     TMAC_MODE_KERNELS(G, KV, decode_u, kUniform)      \
     TMAC_MODE_KERNELS(G, KV, decode_r, kRagged)       \
-    TMAC_MODE_KERNELS(G, KV, layer, kLayer)
+    TMAC_MODE_KERNELS(G, KV, layer, kLayer)         \
+    TMAC_SK_KERNELS(G, KV)
 #else
 #define TMAC_DECODE_F32(G, KV)
 #endif

@@ -107,6 +107,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head_n[kNarrowTypes][3];    // the same: head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> paged[4][2];  // paged caches by kv_dtype: decode, layer step
     std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
+    std::map<std::pair<int, int>, hipFunction_t> decode_sk, combine_sk;  // stream-K ragged decode (fp32)
     // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged, layer, paged layer
     std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
@@ -125,6 +126,7 @@ struct tmac_context {
     int64_t opt_blocked = 0;
     int64_t opt_group_waves = 0;  // 0: automatic (auto_group_waves)
     int64_t opt_mfma = 1;
+    int64_t opt_stream_k = 1;
     std::string last_error;
     char device_name[256] = {0};
 };
@@ -416,6 +418,55 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     return launch(ctx, k.combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
 }
 
+// Schedule of the fp32 ragged decode.  Stream-K (below) pays a pipeline
+// restart and a merge at every sequence change inside a range, so it wins
+// while ranges hold few sequences, and again at many sequences, where the
+// unit grid's serial scan of the lengths dominates.  Measured with lengths
+// uniform in 1..L (unit grid -> stream-K, us): 128 x 8192: 108 -> 93;
+// 256 x 4096: 107 -> 96; 384 x 2048: 97 -> 81; 1024 x 512: 63 -> 83;
+// 1536 x 1024: 148 -> 160; 2048 x 1024: 198 -> 214; 3000 x 40: 237 -> 86;
+// 4096 x 256: 247 -> 177.  Fewer sequences split well on the unit grid:
+// 16 x 32768 59.1 -> 59.6, 64 x 16384 95.6 -> 96.7, 256 x 4096 equal
+// lengths 159.1 -> 160.4.
+bool use_stream_k(const tmac_context* ctx, int n_seq) {
+    if (ctx->opt_stream_k == 0) return false;
+    if (ctx->opt_stream_k == 2) return true;
+    const int64_t n2 = 2 * (int64_t)n_seq;
+    return (n2 >= ctx->n_cu && n2 <= 3 * (int64_t)ctx->n_cu) || n_seq > 10 * ctx->n_cu;
+}
+
+// Stream-K ragged decode (fp32 caches): the kernel cuts the batch's padded
+// row space into `units` equal ranges (one workgroup each, one per CU by
+// default), sized from the lengths on the device, so the total_rows hint is
+// not needed and graph replays may change the lengths.  The combine launch
+// always follows: it merges the sequences spread over several workgroups and
+// writes the outputs of empty and over-long ones.
+int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, hipFunction_t combine, DecodeArgs& a,
+                  int n_seq, int max_len) {
+    a.qscale = kQScale;
+    a.rot_mul = (int)ctx->opt_rot_mul;
+    a.blocked = (int)ctx->opt_blocked;
+    a.err = ctx->err;
+    a.capacity = max_len;
+    if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
+    if (max_len > INT_MAX - kPageRows) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: max_len too large");
+    // One workgroup per CU; two when the sequences outnumber the CUs (more
+    // sequence changes per range, whose stalls the second workgroup covers).
+    const int64_t auto_units = (int64_t)ctx->n_cu * (n_seq > ctx->n_cu ? 2 : 1);
+    const int64_t units = std::min<int64_t>(ctx->opt_target_groups > 0 ? ctx->opt_target_groups : auto_units, 1 << 20);
+    const size_t slot_floats = (size_t)a.n_head * kPartialStride;
+    const size_t slots = (size_t)units + (size_t)n_seq;
+    int rc = ensure_workspace(ctx, stream, slots * slot_floats + 2 * (size_t)n_seq);
+    if (rc) return rc;
+    a.ws = ctx->ws;
+    a.seg_meta = reinterpret_cast<int32_t*>(ctx->ws + slots * slot_floats);
+    a.split_len = 0;
+    a.n_splits = (int)units;
+    a.n_seq = n_seq;
+    if ((rc = launch(ctx, sk, (unsigned)units, 1, 256, stream, &a))) return rc;
+    return launch(ctx, combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
+}
+
 }  // namespace
 
 extern "C" {
@@ -537,6 +588,16 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->combine[m][{sh[0], sh[1]}] = f;
+            if (m == kModeRagged) {
+                std::snprintf(name, sizeof(name), "tmac_decode_sk_g%d_kv%d", sh[0], sh[1]);
+                if ((e = get_function(ctx, &f, name)) != hipSuccess)
+                    return bail(hip_fail(ctx, e, name));
+                ctx->decode_sk[{sh[0], sh[1]}] = f;
+                std::snprintf(name, sizeof(name), "tmac_decode_sk_combine_g%d_kv%d", sh[0], sh[1]);
+                if ((e = get_function(ctx, &f, name)) != hipSuccess)
+                    return bail(hip_fail(ctx, e, name));
+                ctx->combine_sk[{sh[0], sh[1]}] = f;
+            }
             if (m == 0) {
                 std::snprintf(name, sizeof(name), "tmac_prefill_g%d_kv%d", sh[0], sh[1]);
                 if ((e = get_function(ctx, &f, name)) != hipSuccess)
@@ -671,6 +732,12 @@ static int decode_ragged_impl(tmac_context* ctx, tmac_stream stream, int dt, con
     a.offsets = offsets;
     a.lengths = lengths;
     a.n_head = n_head;
+    if (dt == TMAC_KV_F32 && use_stream_k(ctx, n_seq) && ctx->opt_split_len == 0 &&
+        ctx->opt_kernel != TMAC_KERNEL_HEAD && !use_head_kernel(ctx, n_seq, n_head, max_len)) {
+        const std::pair<int, int> key{n_head / n_kv_head, n_kv_head};
+        return run_decode_sk(ctx, (hipStream_t)stream, ctx->decode_sk.at(key), ctx->combine_sk.at(key), a, n_seq,
+                             max_len);
+    }
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head, total_rows);
 }
 
@@ -1137,6 +1204,10 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
         case TMAC_OPT_MFMA_DECODE:
             if (value > 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: MFMA decode is 0 or 1");
             ctx->opt_mfma = value;
+            return TMAC_OK;
+        case TMAC_OPT_STREAM_K:
+            if (value > 2) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: stream-K is 0, 1 or 2");
+            ctx->opt_stream_k = value;
             return TMAC_OK;
         default: return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: unknown option");
     }

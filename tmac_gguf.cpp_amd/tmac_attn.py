@@ -52,6 +52,7 @@ TMAC_OPT_HEAD_WAVES = 5
 TMAC_OPT_WAVE_ORDER = 6
 TMAC_OPT_GROUP_WAVES = 7
 TMAC_OPT_MFMA_DECODE = 8
+TMAC_OPT_STREAM_K = 9
 TMAC_KERNEL_AUTO = 0
 TMAC_KERNEL_GROUP = 1
 TMAC_KERNEL_HEAD = 2
