@@ -599,19 +599,29 @@ __device__ __forceinline__ bool seq_geometry(const DecodeArgs& a, int seq, int& 
 // the unit count never exceeds the n_seq * n_splits grid; the units that carry
 // rows fill the front of the grid (round-robin dispatch then spreads them
 // evenly over the XCDs) and surplus workgroups at the end exit.  Every wave
-// computes the same answer with a 64-lane inclusive scan per 64 sequences.
+// computes the same answer: lane l takes kScanPer consecutive sequences of a
+// round of 64 * kScanPer (their loads all in flight at once), and a 64-lane
+// inclusive scan of the lane sums finds the lane, then the sequence, holding
+// the unit.
+constexpr int kScanPer = 8;
 __device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths, int add, int n_seq,
                                             int split_len, int n_splits, int unit, int& seq, int& split) {
     const int lane = threadIdx.x & 63;
     int base = 0;
-    for (int c0 = 0; c0 < n_seq; c0 += 64) {
-        const int sq = c0 + lane;
-        int u = 0;
-        if (sq < n_seq) {
-            const long long len = (long long)lengths[sq] + add;
-            u = len > 0 ? (int)min((len + split_len - 1) / split_len, (long long)n_splits) : 1;
+    for (int c0 = 0; c0 < n_seq; c0 += 64 * kScanPer) {
+        const int s0 = c0 + lane * kScanPer;
+        int u[kScanPer];
+        int sum = 0;
+#pragma unroll
+        for (int j = 0; j < kScanPer; ++j) {
+            u[j] = 0;
+            if (s0 + j < n_seq) {
+                const long long len = (long long)lengths[s0 + j] + add;
+                u[j] = len > 0 ? (int)min((len + split_len - 1) / split_len, (long long)n_splits) : 1;
+            }
+            sum += u[j];
         }
-        int incl = u;
+        int incl = sum;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const int t = __shfl_up(incl, off);
@@ -621,8 +631,19 @@ __device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths,
         if (unit < base + total) {
             const unsigned long long hit = __ballot(unit < base + incl);
             const int first = __ffsll((long long)hit) - 1;
-            seq = __builtin_amdgcn_readfirstlane(c0 + first);
-            split = __builtin_amdgcn_readfirstlane(unit - base - __shfl(incl - u, first));
+            // Every lane resolves the unit inside its own sequences as if it
+            // were the hit lane; the hit lane's answer is broadcast.
+            int e = base + incl - sum, jj = 0, sp = 0;
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j) {
+                if (unit >= e && unit < e + u[j]) {
+                    jj = j;
+                    sp = unit - e;
+                }
+                e += u[j];
+            }
+            seq = __builtin_amdgcn_readfirstlane(__shfl(s0 + jj, first));
+            split = __builtin_amdgcn_readfirstlane(__shfl(sp, first));
             return true;
         }
         base += total;

@@ -424,8 +424,8 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
 // unit grid's serial scan of the lengths dominates.  Measured with lengths
 // uniform in 1..L (unit grid -> stream-K, us): 128 x 8192: 108 -> 93;
 // 256 x 4096: 107 -> 96; 384 x 2048: 97 -> 81; 1024 x 512: 63 -> 83;
-// 1536 x 1024: 148 -> 160; 2048 x 1024: 198 -> 214; 3000 x 40: 237 -> 86;
-// 4096 x 256: 247 -> 177.  Fewer sequences split well on the unit grid:
+// 1536 x 1024: 148 -> 160; 2048 x 1024: 198 -> 214; 3000 x 40: 180 -> 85;
+// 4096 x 256: 194 -> 178.  Fewer sequences split well on the unit grid:
 // 16 x 32768 59.1 -> 59.6, 64 x 16384 95.6 -> 96.7, 256 x 4096 equal
 // lengths 159.1 -> 160.4.
 bool use_stream_k(const tmac_context* ctx, int n_seq) {
