@@ -479,9 +479,10 @@ def main():
     ap.add_argument("--target-groups", type=int, default=None, help="override TMAC_OPT_TARGET_GROUPS (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
-    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv,kv,paged",
+    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv,kv,paged,ragged",
                     help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv,kv (bf16, "
-                         "fp16, Q8_0 caches), kv16 (bf16, fp16 only), paged")
+                         "fp16, Q8_0 caches), kv16 (bf16, fp16 only), paged, ragged (256 sequences of "
+                         "U[1, 4096] rows, both fp32 ragged schedules)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -528,6 +529,16 @@ def main():
     if "c4" in sections:
         extra["c4"] = bench_c4(ctx, stream, max(10, args.steps // 2), args.warmup)
         log(f"[bench] C4 {extra['c4']['gbs']:.1f} GB/s")
+    if "ragged" in sections:
+        r = {}
+        for name, sk in (("stream_k", 2), ("unit_grid", 0)):
+            ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, sk)
+            r[name] = bench_c4(ctx, stream, max(10, args.steps // 2), args.warmup, n_seq=256, max_len=4096)
+        ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 1)
+        extra["ragged_256"] = r
+        log(f"[bench] ragged 256 x U[1,4096]: stream-K {r['stream_k']['mean_us']:.1f} us "
+            f"({r['stream_k']['gbs']:.0f} GB/s), unit grid {r['unit_grid']['mean_us']:.1f} us "
+            f"({r['unit_grid']['gbs']:.0f} GB/s)")
     for tn in ("bf16", "f16", "q8"):
         if "kv" in sections or ("kv16" in sections and tn != "q8") or f"kv_{tn}" in sections:
             extra[f"c3_{tn}"] = bench_kvn(ctx, stream, args.steps, args.warmup, tn)

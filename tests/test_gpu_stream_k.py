@@ -143,3 +143,62 @@ def test_stream_k_graph_replay_new_lengths(ctx):
     finally:
         ctx.destroy_stream(s)
     assert ctx.check_device_error() == 0
+
+
+def to_pages(k, v, offs, lens, rng, spare=5):
+    """Scatters each sequence's rows over 16-row pages of a pool, in random
+    pool order; returns (k pool, v pool, block table, pages in the pool)."""
+    pr = tmac_attn.PAGE_ROWS
+    need = [(int(n) + pr - 1) // pr for n in lens]
+    n_pages = sum(need) + spare
+    perm = rng.permutation(n_pages)
+    table = np.zeros((lens.size, max(max(need), 1)), np.int32)
+    kp = np.zeros((n_pages * pr, KVD), np.float32)
+    vp = np.zeros_like(kp)
+    nxt = 0
+    for s, n in enumerate(lens):
+        for j in range(need[s]):
+            pg = int(perm[nxt])
+            nxt += 1
+            table[s, j] = pg
+            r = min(int(n) - j * pr, pr)
+            kp[pg * pr:pg * pr + r] = k[offs[s] + j * pr:offs[s] + j * pr + r]
+            vp[pg * pr:pg * pr + r] = v[offs[s] + j * pr:offs[s] + j * pr + r]
+    return kp, vp, table, n_pages
+
+
+@pytest.mark.parametrize("groups", [1, 37, 0])
+def test_stream_k_paged_matches_oracle(ctx, groups):
+    """The stream-K schedule over paged fp32 caches (pages in random pool
+    order), against the oracle on the same rows."""
+    lens, offs, total, k, v, q = ragged_batch(
+        ctx, 4600, [0, 1, 15, 16, 17, 63, 64, 65, 300, 2048, 5000, 0, 33, 7, 4097, 1])
+    ref = reference(q, k, v, offs, lens)
+    kp, vp, table, n_pages = to_pages(k, v, offs, lens, np.random.default_rng(46))
+    dq, dk, dv, dtab, dlen = ctx.upload(q), ctx.upload(kp), ctx.upload(vp), ctx.upload(table), ctx.upload(lens)
+    dout = ctx.empty((lens.size, NH * HD))
+    dout.fill_bytes(0xFF)
+    ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, groups)
+    try:
+        ctx.decode_paged(dq, dk, dv, n_pages, dtab, table.shape[1], dlen, dout, lens.size, NH, NKV, HD,
+                         int(lens.max()))
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, 0)
+    assert_close(dout.numpy(), ref, f"paged stream-K groups={groups}")
+    assert ctx.check_device_error() == 0
+
+
+def test_stream_k_paged_bad_page_is_reported(ctx):
+    """A block-table entry outside the pool is clamped into it (every access
+    stays in bounds) and sets error bit 2; sequences with valid tables are exact."""
+    lens, offs, total, k, v, q = ragged_batch(ctx, 4700, [100, 40, 300])
+    ref = reference(q, k, v, offs, lens)
+    kp, vp, table, n_pages = to_pages(k, v, offs, lens, np.random.default_rng(47))
+    table[1, 1] = n_pages + 3
+    dq, dk, dv, dtab, dlen = ctx.upload(q), ctx.upload(kp), ctx.upload(vp), ctx.upload(table), ctx.upload(lens)
+    dout = ctx.empty((lens.size, NH * HD))
+    ctx.decode_paged(dq, dk, dv, n_pages, dtab, table.shape[1], dlen, dout, lens.size, NH, NKV, HD, 300)
+    keep = np.array([0, 2])
+    assert_close(dout.numpy()[keep], ref[keep], "sequences with valid block tables")
+    assert ctx.check_device_error() == tmac_attn.TMAC_ERR_DEVICE_FAULT
+    assert ctx.check_device_error() == 0

@@ -791,8 +791,11 @@ __device__ __forceinline__ int64_t sk_rows(int len, int max_len) {
 // (uf, ul: the workgroups holding its first and last rows), and workgroup uf
 // records (uf + s, ul - uf + 1) in seg_meta[s] for the combine.  A sequence
 // inside one workgroup's range is written to the output directly.
+// PAGED: the rows live in kPageRows-row pages of a pool (block_table); ranges
+// and segments start at multiples of kPageRows, so a step never straddles a
+// page.
 constexpr int kSkMinRows = 64;
-template <typename T, int G, int KV, int NW, int DEPTH>
+template <typename T, int G, int KV, int NW, int DEPTH, bool PAGED>
 __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
     constexpr int HB = CacheFmt<T>::kHeadBytes;
     constexpr int ROWB = KV * HB;
@@ -907,13 +910,14 @@ __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
         const int64_t r0 = max(lo - P, (int64_t)0), r1 = min(hi - P, (int64_t)len);
         State<G> st;
         state_init(st);
-        const size_t row0 = (size_t)a.offsets[s] + (size_t)r0;
+        const size_t row0 = PAGED ? 0 : (size_t)a.offsets[s] + (size_t)r0;
         const char* kc = reinterpret_cast<const char*>(a.k) + row0 * ROWB;
         const char* vc = reinterpret_cast<const char*>(a.v) + row0 * ROWB;
-        const PageMap pm{nullptr, 0, 0};
+        const PageMap pm{PAGED ? a.block_table + (size_t)s * a.max_pages : nullptr, (int)r0, a.n_pages};
         unsigned bad = 0;
-        attend_rows<T, G, KV, ROWB, NW, DEPTH, false>(kc, vc, (int)(r1 - r0), wave, lane_off, lane_row, lane_col, c,
+        attend_rows<T, G, KV, ROWB, NW, DEPTH, PAGED>(kc, vc, (int)(r1 - r0), wave, lane_off, lane_row, lane_col, c,
                                                      q, st, u * a.rot_mul, a.blocked != 0, pm, bad);
+        if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
         const int uf = (int)min(P / S, (int64_t)last_u);
         const int ul = (int)min((P + len - 1) / S, (int64_t)last_u);
         int s2 = s + 1, len2 = 0;
@@ -1194,7 +1198,7 @@ __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
 // Stream-K ragged decode (fp32 caches) and its combine.
 #define TMAC_SK_KERNELS(G, KV)                                                                     \
     extern "C" __global__ __launch_bounds__(256) void tmac_decode_sk_g##G##_kv##KV(DecodeArgs a) {  \
-        decode_sk_body<float, G, KV, 4, kPrefetchDepth>(a);                                        \
+        decode_sk_body<float, G, KV, 4, kPrefetchDepth, false>(a);                                 \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(64) void tmac_decode_sk_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_sk_body<G, KV>(a);                                                                 \
@@ -1252,6 +1256,9 @@ __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
     TMAC_PAGED_KERNELS(G, KV, bf16, __bf16, kPrefetchDepth16)                           \
     TMAC_PAGED_KERNELS(G, KV, f16, _Float16, kPrefetchDepth16)                          \
     TMAC_PAGED_KERNELS(G, KV, q8, q8_0_t, kPrefetchDepthQ8)                             \
+    extern "C" __global__ __launch_bounds__(256) void tmac_decode_sk_p_f32_g##G##_kv##KV(DecodeArgs a) { \
+        decode_sk_body<float, G, KV, 4, kPrefetchDepth, true>(a);                       \
+    }                                                                                   \
     extern "C" __global__ __launch_bounds__(64) void tmac_decode_p_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, kPaged>(a);                                                 \
     }                                                                                   \

@@ -108,6 +108,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> paged[4][2];  // paged caches by kv_dtype: decode, layer step
     std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
     std::map<std::pair<int, int>, hipFunction_t> decode_sk, combine_sk;  // stream-K ragged decode (fp32)
+    std::map<std::pair<int, int>, hipFunction_t> decode_sk_p;             // the same over paged caches
     // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged, layer, paged layer
     std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
@@ -428,10 +429,15 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
 // 4096 x 256: 194 -> 178.  Fewer sequences split well on the unit grid:
 // 16 x 32768 59.1 -> 59.6, 64 x 16384 95.6 -> 96.7, 256 x 4096 equal
 // lengths 159.1 -> 160.4.
-bool use_stream_k(const tmac_context* ctx, int n_seq) {
+// Paged caches (the unit grid there runs 8-wave workgroups): stream-K wins
+// from half a sequence per CU on: 128 x 8192 111 -> 96, 384 x 2048 99 -> 83,
+// 1024 x 512 79 -> 73, 3000 x 40 178 -> 84, 4096 x 256 320 -> 178; but
+// 16 x 32768 60.4 -> 62.6.
+bool use_stream_k(const tmac_context* ctx, int n_seq, bool paged) {
     if (ctx->opt_stream_k == 0) return false;
     if (ctx->opt_stream_k == 2) return true;
     const int64_t n2 = 2 * (int64_t)n_seq;
+    if (paged) return n2 >= ctx->n_cu;
     return (n2 >= ctx->n_cu && n2 <= 3 * (int64_t)ctx->n_cu) || n_seq > 10 * ctx->n_cu;
 }
 
@@ -562,6 +568,12 @@ int tmac_init(tmac_context** out, int device) {
                     if ((e = get_function(ctx, &f, name)) != hipSuccess)
                         return bail(hip_fail(ctx, e, name));
                     ctx->paged[dt][m][{sh[0], sh[1]}] = f;
+                }
+                if (m == kPagedDecode) {
+                    std::snprintf(name, sizeof(name), "tmac_decode_sk_p_f32_g%d_kv%d", sh[0], sh[1]);
+                    if ((e = get_function(ctx, &f, name)) != hipSuccess)
+                        return bail(hip_fail(ctx, e, name));
+                    ctx->decode_sk_p[{sh[0], sh[1]}] = f;
                 }
                 std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", pp, sh[0], sh[1]);
                 if ((e = get_function(ctx, &f, name)) != hipSuccess)
@@ -732,7 +744,7 @@ static int decode_ragged_impl(tmac_context* ctx, tmac_stream stream, int dt, con
     a.offsets = offsets;
     a.lengths = lengths;
     a.n_head = n_head;
-    if (dt == TMAC_KV_F32 && use_stream_k(ctx, n_seq) && ctx->opt_split_len == 0 &&
+    if (dt == TMAC_KV_F32 && use_stream_k(ctx, n_seq, false) && ctx->opt_split_len == 0 &&
         ctx->opt_kernel != TMAC_KERNEL_HEAD && !use_head_kernel(ctx, n_seq, n_head, max_len)) {
         const std::pair<int, int> key{n_head / n_kv_head, n_kv_head};
         return run_decode_sk(ctx, (hipStream_t)stream, ctx->decode_sk.at(key), ctx->combine_sk.at(key), a, n_seq,
@@ -871,6 +883,11 @@ int tmac_attention_decode_paged(tmac_context* ctx, tmac_stream stream, int kv_dt
     a.block_table = block_table;
     a.max_pages = max_pages;
     a.n_pages = n_pages;
+    if (kv_dtype == TMAC_KV_F32 && use_stream_k(ctx, n_seq, true) && ctx->opt_split_len == 0) {
+        const std::pair<int, int> key{n_head / n_kv_head, n_kv_head};
+        return run_decode_sk(ctx, (hipStream_t)stream, ctx->decode_sk_p.at(key), ctx->combine_sk.at(key), a, n_seq,
+                             max_len);
+    }
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head, total_rows);
 }
 
