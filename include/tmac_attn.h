@@ -330,11 +330,12 @@ enum tmac_option {
     TMAC_OPT_GROUP_WAVES = 7,   /* fp32 group kernel workgroup size in waves: 4 or 8; 0 (default) = 4 unless a
                                    split would hold fewer than 64 rows, then 8 */
     TMAC_OPT_MFMA_DECODE = 8,   /* 1 (default): bf16/fp16/Q8_0 caches use the MFMA group kernel (decode and layer step) where one exists; 0: VALU */
-    TMAC_OPT_STREAM_K = 9       /* fp32 ragged and paged decode schedule: 1 (default) = automatic, 2 = always
-                                   stream-K (the batch's rows cut into equal ranges, one workgroup each), 0 = never
-                                   (one workgroup per (sequence, split) unit).  Stream-K is not used when
-                                   TMAC_OPT_SPLIT_LEN is set or the head kernel is chosen; automatic picks it for
-                                   0.5 to 1.5 sequences per CU or more than 10 (ragged), from 0.5 (paged) */
+    TMAC_OPT_STREAM_K = 9       /* ragged and paged decode schedule: 1 (default) = automatic, 2 = always stream-K
+                                   (the batch's rows cut into equal ranges, one workgroup each), 0 = never (one
+                                   workgroup per (sequence, split) unit).  Stream-K is not used when
+                                   TMAC_OPT_SPLIT_LEN is set, the head kernel is chosen or (narrow caches) the MFMA
+                                   decode is off; automatic picks it, in sequences per CU, for 0.5 to 1.5 or more
+                                   than 10 (fp32 ragged), from 0.5 (fp32 paged), above 10 (bf16 / fp16 / Q8_0) */
 };
 enum tmac_kernel_choice {
     TMAC_KERNEL_AUTO = 0,   /* head kernel for short contexts on few sequences, else group */

@@ -17,6 +17,7 @@ import pytest
 import oracle
 import tmac_attn
 from conftest import assert_close
+from test_gpu_kv_q8_paged import data, store, widen
 
 pytestmark = pytest.mark.gpu
 
@@ -153,7 +154,7 @@ def to_pages(k, v, offs, lens, rng, spare=5):
     n_pages = sum(need) + spare
     perm = rng.permutation(n_pages)
     table = np.zeros((lens.size, max(max(need), 1)), np.int32)
-    kp = np.zeros((n_pages * pr, KVD), np.float32)
+    kp = np.zeros((n_pages * pr,) + k.shape[1:], k.dtype)
     vp = np.zeros_like(kp)
     nxt = 0
     for s, n in enumerate(lens):
@@ -201,4 +202,43 @@ def test_stream_k_paged_bad_page_is_reported(ctx):
     keep = np.array([0, 2])
     assert_close(dout.numpy()[keep], ref[keep], "sequences with valid block tables")
     assert ctx.check_device_error() == tmac_attn.TMAC_ERR_DEVICE_FAULT
+    assert ctx.check_device_error() == 0
+
+
+NARROW = [tmac_attn.TMAC_KV_BF16, tmac_attn.TMAC_KV_F16, tmac_attn.TMAC_KV_Q8_0]
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("dt", NARROW)
+def test_stream_k_mfma_matches_oracle(ctx, dt, paged):
+    """The stream-K schedule on the MFMA decode (bf16 / fp16 / Q8_0 caches),
+    contiguous ragged and paged, for 1, 37 and one-per-CU workgroups, against
+    the oracle over the cache's exactly widened rows.  Rows of very different
+    magnitudes exercise the Q8_0 block scales."""
+    lens = np.array([0, 1, 15, 16, 17, 63, 64, 65, 300, 2048, 5000, 0, 33, 7, 4097, 1], np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens[:-1], dtype=np.int64)]).astype(np.int64)
+    total = int(lens.sum())
+    kb = store(data(4800 + dt, (total, KVD), 3), dt)
+    vb = store(data(4810 + dt, (total, KVD), 3), dt)
+    q = data(4820 + dt, (lens.size, NH * HD))
+    ref = reference(q, widen(kb, dt), widen(vb, dt), offs, lens)
+    dq, dlen, dout = ctx.upload(q), ctx.upload(lens), ctx.empty((lens.size, NH * HD))
+    if paged:
+        kp, vp, table, n_pages = to_pages(kb, vb, offs, lens, np.random.default_rng(48))
+        dk, dv, dtab = ctx.upload(kp), ctx.upload(vp), ctx.upload(table)
+    else:
+        dk, dv, doff = ctx.upload(kb), ctx.upload(vb), ctx.upload(offs)
+    try:
+        for groups in (1, 37, 0):
+            ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, groups)
+            dout.fill_bytes(0xFF)
+            if paged:
+                ctx.decode_paged(dq, dk, dv, n_pages, dtab, table.shape[1], dlen, dout, lens.size, NH, NKV, HD,
+                                 int(lens.max()), kv_dtype=dt)
+            else:
+                ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, lens.size, NH, NKV, HD, int(lens.max()),
+                                  kv_dtype=dt)
+            assert_close(dout.numpy(), ref, f"MFMA stream-K dt={dt} paged={paged} groups={groups}")
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, 0)
     assert ctx.check_device_error() == 0

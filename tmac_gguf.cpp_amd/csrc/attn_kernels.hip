@@ -791,19 +791,20 @@ __device__ __forceinline__ int64_t sk_rows(int len, int max_len) {
 // (uf, ul: the workgroups holding its first and last rows), and workgroup uf
 // records (uf + s, ul - uf + 1) in seg_meta[s] for the combine.  A sequence
 // inside one workgroup's range is written to the output directly.
-// PAGED: the rows live in kPageRows-row pages of a pool (block_table); ranges
-// and segments start at multiples of kPageRows, so a step never straddles a
-// page.
+// Paged caches: ranges and segments start at multiples of kPageRows, so a
+// step or tile never straddles a page.
 constexpr int kSkMinRows = 64;
-template <typename T, int G, int KV, int NW, int DEPTH, bool PAGED>
-__device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
-    constexpr int HB = CacheFmt<T>::kHeadBytes;
-    constexpr int ROWB = KV * HB;
-    constexpr int NH = KV * G;
-    constexpr int NT = NW * 64;
+
+// This workgroup's range [lo, hi) of the row space, S, the last workgroup
+// with rows, and the sequence holding row lo with its first row (s0, P0).
+// False when the row space ends before the range.  NT threads, all of which
+// must call it.
+template <int NT>
+__device__ __forceinline__ bool sk_locate(const DecodeArgs& a, int64_t& S, int64_t& lo, int64_t& hi, int& last_u,
+                                          int& s0, int64_t& P0) {
+    constexpr int NW = NT / 64;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int u = blockIdx.x;
     __shared__ int64_t s_wsum[NW];
     __shared__ int64_t s_hit[2];  // (sequence, its first row)
 
@@ -829,12 +830,13 @@ __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
     int64_t R = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) R += s_wsum[w];
-    int64_t S = (R + gridDim.x - 1) / gridDim.x;
+    S = (R + gridDim.x - 1) / gridDim.x;
     S = max((S + kPageRows - 1) & ~(int64_t)(kPageRows - 1), (int64_t)kSkMinRows);
-    const int64_t lo = (int64_t)u * S, hi = lo + S;
-    const int last_u = (int)min((R - 1) / S, (int64_t)gridDim.x - 1);  // last workgroup with rows
-    if (lo >= R) return;  // uniform: every thread has the same R
-    __syncthreads();      // s_wsum is reused below
+    lo = (int64_t)blockIdx.x * S;
+    hi = lo + S;
+    last_u = (int)min((R - 1) / S, (int64_t)gridDim.x - 1);
+    if (lo >= R) return false;  // uniform: every thread has the same R
+    __syncthreads();            // s_wsum is reused below
 
     // 2. The sequence holding row lo, and its first row: a workgroup-wide
     //    inclusive scan of the padded lengths, NT sequences per round, until a
@@ -873,33 +875,63 @@ __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
         if (s_hit[0] >= 0) break;
         base += total;
     }
+    s0 = (int)s_hit[0];
+    P0 = s_hit[1];
+    return true;
+}
 
-    // 3. One segment per sequence overlapping [lo, hi).  The next segment's
-    //    query is loaded before this one's merge, so its latency overlaps it.
+// Advances (s, P) to the first sequence from s on with rows in [lo, hi)
+// (P: its first row in the row space, len: its length); false when there is
+// none.  The values are uniform, so they are kept in scalar registers.
+__device__ __forceinline__ bool sk_seek(const DecodeArgs& a, int64_t lo, int64_t hi, int& s, int64_t& P, int& len) {
+    for (; s < a.n_seq && P < hi; ++s) {
+        s = __builtin_amdgcn_readfirstlane(s);
+        len = __builtin_amdgcn_readfirstlane(a.lengths[s]);
+        const int64_t rows = sk_rows(len, a.capacity);
+        if (rows > 0 && lo - P < (int64_t)len) return true;  // lo - P < len: a row of s lies in [lo, hi)
+        P += rows;
+    }
+    return false;
+}
+
+// The combine's record for sequence s (first workspace slot, slots used),
+// written by the workgroup holding its first row; returns true when the
+// sequence lies inside this workgroup's range (its output is written
+// directly).  Segment slot of workgroup u: u + s.
+__device__ __forceinline__ bool sk_record(const DecodeArgs& a, int s, int64_t P, int len, int64_t S, int last_u) {
+    const int uf = (int)min(P / S, (int64_t)last_u);
+    const int ul = (int)min((P + len - 1) / S, (int64_t)last_u);
+    if ((int)blockIdx.x == uf && threadIdx.x == 0) {
+        a.seg_meta[2 * s] = uf + s;
+        a.seg_meta[2 * s + 1] = ul - uf + 1;
+    }
+    return uf == ul;
+}
+
+// Stream-K decode, VALU group kernel (fp32 caches).  The next segment's query
+// is loaded before this one's merge, so its latency overlaps the merge.
+template <typename T, int G, int KV, int NW, int DEPTH, bool PAGED>
+__device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
+    constexpr int HB = CacheFmt<T>::kHeadBytes;
+    constexpr int ROWB = KV * HB;
+    constexpr int NH = KV * G;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int u = blockIdx.x;
+    int64_t S, lo, hi, P;
+    int last_u, s, len = 0;
+    if (!sk_locate<NW * 64>(a, S, lo, hi, last_u, s, P)) return;
+    if (!sk_seek(a, lo, hi, s, P, len)) return;
+
     const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
     const int lane_row = slot / KV;
     const int kvh = slot % KV;
     const int lane_col = kvh * HB + 4 * c * CacheFmt<T>::kDimBytes;
     const int lane_off = lane_row * ROWB + lane_col;
-    // Advances (s, P) to the first sequence from s on with rows in [lo, hi);
-    // false when there is none.  len: its length.
-    auto seek = [&](int& s, int64_t& P, int& len) -> bool {
-        for (; s < a.n_seq && P < hi; ++s) {
-            s = __builtin_amdgcn_readfirstlane(s);
-            len = __builtin_amdgcn_readfirstlane(a.lengths[s]);
-            const int64_t rows = sk_rows(len, a.capacity);
-            if (rows > 0 && lo - P < (int64_t)len) return true;  // lo - P < len: a row of s lies in [lo, hi)
-            P += rows;
-        }
-        return false;
-    };
-    auto load_q = [&](float (&q)[G][kDimsPerLane], int s) {
+    auto load_q = [&](float (&q)[G][kDimsPerLane], int sq) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) load8(q[g], a.q + ((size_t)s * NH + kvh * G + g) * kHeadDim + 4 * c);
+        for (int g = 0; g < G; ++g) load8(q[g], a.q + ((size_t)sq * NH + kvh * G + g) * kHeadDim + 4 * c);
     };
-    int s = (int)s_hit[0], len = 0;
-    int64_t P = s_hit[1];
-    if (!seek(s, P, len)) return;
     float q[G][kDimsPerLane];
     load_q(q, s);
     while (true) {
@@ -918,17 +950,11 @@ __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
         attend_rows<T, G, KV, ROWB, NW, DEPTH, PAGED>(kc, vc, (int)(r1 - r0), wave, lane_off, lane_row, lane_col, c,
                                                      q, st, u * a.rot_mul, a.blocked != 0, pm, bad);
         if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
-        const int uf = (int)min(P / S, (int64_t)last_u);
-        const int ul = (int)min((P + len - 1) / S, (int64_t)last_u);
+        const bool direct = sk_record(a, s, P, len, S, last_u);
         int s2 = s + 1, len2 = 0;
         int64_t P2 = P + sk_rows(len, a.capacity);
-        const bool more = seek(s2, P2, len2);
+        const bool more = sk_seek(a, lo, hi, s2, P2, len2);
         if (more) load_q(q, s2);
-        if (u == uf && threadIdx.x == 0) {
-            a.seg_meta[2 * s] = uf + s;
-            a.seg_meta[2 * s + 1] = ul - uf + 1;
-        }
-        const bool direct = uf == ul;
         float* ws_slot = direct ? nullptr : a.ws + (size_t)(u + s) * NH * kPartialStride;
         finish<G, KV, NW>(st, lane, wave, direct, a.out + (size_t)s * NH * kHeadDim, ws_slot);
         if (!more) break;
@@ -1927,8 +1953,15 @@ __device__ __forceinline__ void mtile_load_any(typename MTraits<T, KV>::Tile& t,
         mtile_load<T, KV>(t, kbase, vbase, valid, lane);
 }
 
+// One MFMA decode segment: rows r0 .. r0 + n_rows - 1 of sequence seq (base:
+// its first cache row in the contiguous modes), merged over the waves and
+// written to out_heads (ws_split null) or as this split's partial.  split and
+// n_act matter in the layer modes only (the last split writes the new row).
+// Every thread of the workgroup calls it.
 template <typename T, int G, int KV, int MODE>
-__device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
+__device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, int split, int n_act, int pos,
+                                                size_t base, int r0, int n_rows, float* __restrict__ out_heads,
+                                                float* __restrict__ ws_split) {
     constexpr bool Q8 = __is_same(T, q8_0_t);
     using Tile = typename MTraits<T, KV>::Tile;
     using M = typename MTraits<T, KV>::Ops;
@@ -1943,39 +1976,6 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, g = lane >> 4;
-    int split = blockIdx.x, seq = blockIdx.y;
-    if (MODE == kRagged || PAGED) {
-        const bool by_pos = MODE == kPagedLayer;
-        if (!ragged_unit(by_pos ? a.positions : a.lengths, by_pos ? 1 : 0, a.n_seq, a.split_len, a.n_splits,
-                         blockIdx.x, seq, split))
-            return;
-    }
-    int n_pos, pos;
-    size_t base;
-    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) {
-        if (split == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
-        return;
-    }
-    n_pos = __builtin_amdgcn_readfirstlane(n_pos);
-    pos = __builtin_amdgcn_readfirstlane(pos);
-    float* out_heads = a.out + (size_t)seq * NH * kHeadDim;
-    if (n_pos <= 0) {
-        if (split == 0)
-            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_heads[i] = 0.f;
-        return;
-    }
-    const int n_act = (n_pos + a.split_len - 1) / a.split_len;
-    if (n_act > a.n_splits) {
-        if (split == 0) {
-            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_heads[i] = __builtin_nanf("");
-            if (threadIdx.x == 0) atomicOr(a.err, 2);
-        }
-        return;
-    }
-    if (split >= n_act) return;
-    const int r0 = split * a.split_len;
-    const int mem_rows = LAYER ? pos : n_pos;  // layer modes: row `pos` is the new token, attended from registers
-    const int n_rows = max(min(r0 + a.split_len, mem_rows) - r0, 0);
     const float2* cs_row = LAYER ? a.rope_cs + (size_t)pos * (kHeadDim / 2) : nullptr;
 
     // Q^T operands: column col, dims 32 (b % 2) + 8 g + 0..7 of kv head b / 2,
@@ -2309,9 +2309,74 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
         }
     }
     __syncthreads();
+    merge_waves<NH, NP, NW * 64>(s_acc, s_m, s_l, ws_split == nullptr, out_heads, ws_split);
+}
+
+// MFMA decode for one (split, sequence) workgroup (flat unit grid in the
+// ragged and paged modes).
+template <typename T, int G, int KV, int MODE>
+__device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
+    constexpr int NH = KV * G;
+    constexpr int NW = kMWaves;
+    constexpr bool PAGED = is_paged(MODE);
+    constexpr bool LAYER = is_layer(MODE);
+    int split = blockIdx.x, seq = blockIdx.y;
+    if (MODE == kRagged || PAGED) {
+        const bool by_pos = MODE == kPagedLayer;
+        if (!ragged_unit(by_pos ? a.positions : a.lengths, by_pos ? 1 : 0, a.n_seq, a.split_len, a.n_splits,
+                         blockIdx.x, seq, split))
+            return;
+    }
+    int n_pos, pos;
+    size_t base;
+    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) {
+        if (split == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
+        return;
+    }
+    n_pos = __builtin_amdgcn_readfirstlane(n_pos);
+    pos = __builtin_amdgcn_readfirstlane(pos);
+    float* out_heads = a.out + (size_t)seq * NH * kHeadDim;
+    if (n_pos <= 0) {
+        if (split == 0)
+            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_heads[i] = 0.f;
+        return;
+    }
+    const int n_act = (n_pos + a.split_len - 1) / a.split_len;
+    if (n_act > a.n_splits) {
+        if (split == 0) {
+            for (int i = threadIdx.x; i < NH * kHeadDim; i += NW * 64) out_heads[i] = __builtin_nanf("");
+            if (threadIdx.x == 0) atomicOr(a.err, 2);
+        }
+        return;
+    }
+    if (split >= n_act) return;
+    const int r0 = split * a.split_len;
+    const int mem_rows = LAYER ? pos : n_pos;  // layer modes: row `pos` is the new token, attended from registers
+    const int n_rows = max(min(r0 + a.split_len, mem_rows) - r0, 0);
     const bool direct = (n_act == 1);
     float* ws_split = direct ? nullptr : a.ws + ((size_t)seq * a.n_splits + split) * NH * kPartialStride;
-    merge_waves<NH, NP, NW * 64>(s_acc, s_m, s_l, direct, out_heads, ws_split);
+    mdecode_segment<T, G, KV, MODE>(a, seq, split, n_act, pos, base, r0, n_rows, out_heads, ws_split);
+}
+
+// Stream-K decode on the MFMA kernel (bf16 / fp16 / Q8_0 caches, ragged or
+// paged): one mdecode_segment per sequence overlapping this workgroup's range
+// of the row space.
+template <typename T, int G, int KV, bool PAGED>
+__device__ __forceinline__ void mdecode_sk_body(const DecodeArgs& a) {
+    constexpr int NH = KV * G;
+    int64_t S, lo, hi, P;
+    int last_u, s, len = 0;
+    if (!sk_locate<kMWaves * 64>(a, S, lo, hi, last_u, s, P)) return;
+    for (bool first = true; sk_seek(a, lo, hi, s, P, len); ++s, first = false) {
+        if (!first) __syncthreads();  // the previous segment's merge reads the LDS this one's tiles reuse
+        const int64_t r0 = max(lo - P, (int64_t)0), r1 = min(hi - P, (int64_t)len);
+        const bool direct = sk_record(a, s, P, len, S, last_u);
+        float* ws_slot = direct ? nullptr : a.ws + ((size_t)blockIdx.x + s) * NH * kPartialStride;
+        mdecode_segment<T, G, KV, PAGED ? kPaged : kRagged>(a, s, 0, 1, 0, PAGED ? 0 : (size_t)a.offsets[s],
+                                                            (int)r0, (int)(r1 - r0),
+                                                            a.out + (size_t)s * NH * kHeadDim, ws_slot);
+        P += sk_rows(len, a.capacity);
+    }
 }
 
 #define TMAC_MDECODE_KERNELS_T(G, KV, TN, T)                                                          \
@@ -2334,6 +2399,14 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_pl_##TN##_g##G##_kv##KV(    \
         DecodeArgs a) {                                                                                \
         mdecode_body<T, G, KV, kPagedLayer>(a);                                                        \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_sk_##TN##_g##G##_kv##KV(    \
+        DecodeArgs a) {                                                                                \
+        mdecode_sk_body<T, G, KV, false>(a);                                                           \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_sk_p_##TN##_g##G##_kv##KV(  \
+        DecodeArgs a) {                                                                                \
+        mdecode_sk_body<T, G, KV, true>(a);                                                            \
     }
 #define TMAC_MDECODE_KERNELS(G, KV)               \
     TMAC_MDECODE_KERNELS_T(G, KV, bf16, __bf16)    \

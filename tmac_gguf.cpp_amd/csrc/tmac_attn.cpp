@@ -109,6 +109,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
     std::map<std::pair<int, int>, hipFunction_t> decode_sk, combine_sk;  // stream-K ragged decode (fp32)
     std::map<std::pair<int, int>, hipFunction_t> decode_sk_p;             // the same over paged caches
+    std::map<std::pair<int, int>, hipFunction_t> mdecode_sk[kNarrowTypes][2];  // MFMA stream-K: ragged, paged
     // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged, layer, paged layer
     std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
@@ -433,12 +434,39 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
 // from half a sequence per CU on: 128 x 8192 111 -> 96, 384 x 2048 99 -> 83,
 // 1024 x 512 79 -> 73, 3000 x 40 178 -> 84, 4096 x 256 320 -> 178; but
 // 16 x 32768 60.4 -> 62.6.
-bool use_stream_k(const tmac_context* ctx, int n_seq, bool paged) {
+// MFMA decode (bf16 / fp16 / Q8_0 caches, ragged or paged): a segment's setup
+// (query split into parts, tiles spread over 8 waves, LDS merge) is heavier,
+// so only the many-sequence case gains: bf16 3000 x 40 144 -> 105, Q8_0
+// 154 -> 120; but bf16 384 x 2048 53 -> 64, 1024 x 512 54 -> 81, 2048 x 512
+// 119 -> 124, Q8_0 1024 x 512 61 -> 81.
+enum SkKind { kSkF32Ragged, kSkF32Paged, kSkMfma };
+bool use_stream_k(const tmac_context* ctx, int n_seq, SkKind kind) {
     if (ctx->opt_stream_k == 0) return false;
     if (ctx->opt_stream_k == 2) return true;
     const int64_t n2 = 2 * (int64_t)n_seq;
-    if (paged) return n2 >= ctx->n_cu;
-    return (n2 >= ctx->n_cu && n2 <= 3 * (int64_t)ctx->n_cu) || n_seq > 10 * ctx->n_cu;
+    if (kind == kSkF32Paged) return n2 >= ctx->n_cu;
+    const bool many = n_seq > 10 * ctx->n_cu;
+    if (kind == kSkMfma) return many;
+    return (n2 >= ctx->n_cu && n2 <= 3 * (int64_t)ctx->n_cu) || many;
+}
+
+// Stream-K kernel for a ragged (paged = false) or paged batch of cache type
+// dt and its block size, or null when the schedule does not apply.
+hipFunction_t stream_k_kernel(const tmac_context* ctx, int dt, bool paged, int n_seq, int n_head, int n_kv_head,
+                              unsigned* threads) {
+    const SkKind kind = dt != TMAC_KV_F32 ? kSkMfma : paged ? kSkF32Paged : kSkF32Ragged;
+    if (ctx->opt_split_len != 0 || !use_stream_k(ctx, n_seq, kind)) return nullptr;
+    const std::pair<int, int> key{n_head / n_kv_head, n_kv_head};
+    if (dt == TMAC_KV_F32) {
+        *threads = 256;
+        return (paged ? ctx->decode_sk_p : ctx->decode_sk).at(key);
+    }
+    if (!ctx->opt_mfma) return nullptr;
+    const auto& tab = ctx->mdecode_sk[dt - 1][paged ? 1 : 0];
+    const auto it = tab.find(key);
+    if (it == tab.end()) return nullptr;
+    *threads = tmac::kMWavesHost * 64;
+    return it->second;
 }
 
 // Stream-K ragged decode (fp32 caches): the kernel cuts the batch's padded
@@ -447,8 +475,8 @@ bool use_stream_k(const tmac_context* ctx, int n_seq, bool paged) {
 // not needed and graph replays may change the lengths.  The combine launch
 // always follows: it merges the sequences spread over several workgroups and
 // writes the outputs of empty and over-long ones.
-int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, hipFunction_t combine, DecodeArgs& a,
-                  int n_seq, int max_len) {
+int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, unsigned threads, hipFunction_t combine,
+                  DecodeArgs& a, int n_seq, int max_len) {
     a.qscale = kQScale;
     a.rot_mul = (int)ctx->opt_rot_mul;
     a.blocked = (int)ctx->opt_blocked;
@@ -469,7 +497,7 @@ int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, hipFu
     a.split_len = 0;
     a.n_splits = (int)units;
     a.n_seq = n_seq;
-    if ((rc = launch(ctx, sk, (unsigned)units, 1, 256, stream, &a))) return rc;
+    if ((rc = launch(ctx, sk, (unsigned)units, 1, threads, stream, &a))) return rc;
     return launch(ctx, combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
 }
 
@@ -559,6 +587,11 @@ int tmac_init(tmac_context** out, int device) {
                 for (int mi = m; mi < 5; mi += 3) {  // m = 0, 1, 2 -> modes m and m + 3
                     std::snprintf(name, sizeof(name), "%s_%s_g%d_kv%d", mp[mi], kTypeName[dt + 1], sh[0], sh[1]);
                     if (get_function(ctx, &f, name) == hipSuccess) ctx->mdecode[dt][mi][{sh[0], sh[1]}] = f;
+                }
+                if (m < 2) {  // stream-K: m = 0 ragged, 1 paged
+                    std::snprintf(name, sizeof(name), "tmac_mdecode_sk%s_%s_g%d_kv%d", m ? "_p" : "",
+                                  kTypeName[dt + 1], sh[0], sh[1]);
+                    if (get_function(ctx, &f, name) == hipSuccess) ctx->mdecode_sk[dt][m][{sh[0], sh[1]}] = f;
                 }
             }
             if (m < 2) {  // paged kernels: m = kPagedDecode, kPagedLayer
@@ -744,11 +777,11 @@ static int decode_ragged_impl(tmac_context* ctx, tmac_stream stream, int dt, con
     a.offsets = offsets;
     a.lengths = lengths;
     a.n_head = n_head;
-    if (dt == TMAC_KV_F32 && use_stream_k(ctx, n_seq, false) && ctx->opt_split_len == 0 &&
-        ctx->opt_kernel != TMAC_KERNEL_HEAD && !use_head_kernel(ctx, n_seq, n_head, max_len)) {
-        const std::pair<int, int> key{n_head / n_kv_head, n_kv_head};
-        return run_decode_sk(ctx, (hipStream_t)stream, ctx->decode_sk.at(key), ctx->combine_sk.at(key), a, n_seq,
-                             max_len);
+    unsigned threads = 0;
+    if (ctx->opt_kernel != TMAC_KERNEL_HEAD && !use_head_kernel(ctx, n_seq, n_head, max_len)) {
+        if (hipFunction_t sk = stream_k_kernel(ctx, dt, false, n_seq, n_head, n_kv_head, &threads))
+            return run_decode_sk(ctx, (hipStream_t)stream, sk, threads,
+                                 ctx->combine_sk.at({n_head / n_kv_head, n_kv_head}), a, n_seq, max_len);
     }
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head, total_rows);
 }
@@ -883,11 +916,10 @@ int tmac_attention_decode_paged(tmac_context* ctx, tmac_stream stream, int kv_dt
     a.block_table = block_table;
     a.max_pages = max_pages;
     a.n_pages = n_pages;
-    if (kv_dtype == TMAC_KV_F32 && use_stream_k(ctx, n_seq, true) && ctx->opt_split_len == 0) {
-        const std::pair<int, int> key{n_head / n_kv_head, n_kv_head};
-        return run_decode_sk(ctx, (hipStream_t)stream, ctx->decode_sk_p.at(key), ctx->combine_sk.at(key), a, n_seq,
-                             max_len);
-    }
+    unsigned threads = 0;
+    if (hipFunction_t sk = stream_k_kernel(ctx, kv_dtype, true, n_seq, n_head, n_kv_head, &threads))
+        return run_decode_sk(ctx, (hipStream_t)stream, sk, threads, ctx->combine_sk.at({n_head / n_kv_head, n_kv_head}),
+                             a, n_seq, max_len);
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head, total_rows);
 }
 
