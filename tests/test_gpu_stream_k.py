@@ -242,3 +242,22 @@ def test_stream_k_mfma_matches_oracle(ctx, dt, paged):
     finally:
         ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, 0)
     assert ctx.check_device_error() == 0
+
+
+def test_stream_k_single_long_sequence(ctx):
+    """One 16,384-row sequence over every workgroup (64-row ranges: 256
+    partials, merged by the combine in chunks of 32), then the same rows as
+    two sequences split mid-range."""
+    lens, offs, total, k, v, q = ragged_batch(ctx, 4900, [16384])
+    ref = reference(q, k, v, offs, lens)
+    dq, dk, dv, doff, dlen = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.upload(offs), ctx.upload(lens)
+    dout = ctx.empty((1, NH * HD))
+    ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, 1, NH, NKV, HD, 16384)
+    assert_close(dout.numpy(), ref, "one sequence over all workgroups")
+    lens2 = np.array([10001, 6383], np.int32)
+    offs2 = np.array([0, 10001], np.int64)
+    q2 = oracle.normal(4903, (2, NH * HD))
+    dq2, dout2 = ctx.upload(q2), ctx.empty((2, NH * HD))
+    ctx.decode_ragged(dq2, dk, dv, ctx.upload(offs2), ctx.upload(lens2), dout2, 2, NH, NKV, HD, 10001)
+    assert_close(dout2.numpy(), reference(q2, k, v, offs2, lens2), "two sequences of the same rows")
+    assert ctx.check_device_error() == 0
