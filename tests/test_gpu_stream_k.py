@@ -261,3 +261,26 @@ def test_stream_k_single_long_sequence(ctx):
     ctx.decode_ragged(dq2, dk, dv, ctx.upload(offs2), ctx.upload(lens2), dout2, 2, NH, NKV, HD, 10001)
     assert_close(dout2.numpy(), reference(q2, k, v, offs2, lens2), "two sequences of the same rows")
     assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_stream_k_no_rows(ctx, paged):
+    """Batches with no rows to attend: all sequences empty (zeros), then all
+    longer than max_len (NaN and error bit 1).  No workgroup has a range;
+    the combine writes every output."""
+    k = oracle.normal(5000, (64, KVD))
+    table = np.arange(4, dtype=np.int32).reshape(1, 4).repeat(3, 0)
+    dk, dv, dtab = ctx.upload(k), ctx.upload(k), ctx.upload(table)
+    doff = ctx.upload(np.zeros(3, np.int64))
+    dq, dout = ctx.upload(oracle.normal(5001, (3, NH * HD))), ctx.empty((3, NH * HD))
+    for lens, want_err in ((np.zeros(3, np.int32), 0), (np.full(3, 60, np.int32), tmac_attn.TMAC_ERR_DEVICE_FAULT)):
+        dout.fill_bytes(0x3F)
+        dlen = ctx.upload(lens)
+        if paged:
+            ctx.decode_paged(dq, dk, dv, 4, dtab, 4, dlen, dout, 3, NH, NKV, HD, 48)
+        else:
+            ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, 3, NH, NKV, HD, 48)
+        got = dout.numpy()
+        assert np.all(got == 0) if want_err == 0 else np.all(np.isnan(got))
+        assert ctx.check_device_error() == want_err
+    assert ctx.check_device_error() == 0
