@@ -335,7 +335,8 @@ enum tmac_option {
                                    workgroup per (sequence, split) unit).  Stream-K is not used when
                                    TMAC_OPT_SPLIT_LEN is set, the head kernel is chosen or (narrow caches) the MFMA
                                    decode is off; automatic picks it, in sequences per CU, for 0.5 to 1.5 or more
-                                   than 10 (fp32 ragged), from 0.5 (fp32 paged), above 10 (bf16 / fp16 / Q8_0) */
+                                   than 10 (fp32 ragged), from 0.5 (fp32 paged), up to 2 or more than 10 (fp32
+                                   paged layer step), above 10 (bf16 / fp16 / Q8_0) */
 };
 enum tmac_kernel_choice {
     TMAC_KERNEL_AUTO = 0,   /* head kernel for short contexts on few sequences, else group */

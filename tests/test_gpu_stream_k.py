@@ -17,12 +17,13 @@ import pytest
 import oracle
 import tmac_attn
 from conftest import assert_close
-from test_gpu_kv_q8_paged import data, store, widen
+from test_gpu_kv_q8_paged import build_pool, data, store, widen
 
 pytestmark = pytest.mark.gpu
 
 NH, NKV, HD = 14, 2, 64
 KVD = NKV * HD
+PR = tmac_attn.PAGE_ROWS
 
 
 @pytest.fixture(autouse=True)
@@ -283,4 +284,64 @@ def test_stream_k_no_rows(ctx, paged):
         got = dout.numpy()
         assert np.all(got == 0) if want_err == 0 else np.all(np.isnan(got))
         assert ctx.check_device_error() == want_err
+    assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("groups", [1, 37, 0])
+def test_stream_k_paged_layer_step(ctx, groups):
+    """The batched paged layer step (fp32) on the stream-K schedule: sequences
+    at positions from 0 to 2,999 (page boundaries among them) get RoPE, their
+    new row written into its page and attention over rows 0..pos; the segment
+    holding row pos takes the new token.  Outputs against the oracle, pools
+    byte for byte."""
+    f32 = tmac_attn.TMAC_KV_F32
+    rng = np.random.default_rng(52 + groups)
+    positions = rng.integers(0, 3000, 40).astype(np.int32)
+    positions[:6] = [0, 1, 15, 16, 31, 2047]
+    n_seq = positions.size
+    max_len = int(positions.max()) + 1
+    k_rows = [data(5100 + s, (int(p) + 1, KVD)) for s, p in enumerate(positions)]
+    v_rows = [data(5200 + s, (int(p) + 1, KVD)) for s, p in enumerate(positions)]
+    n_pages = int(sum((p + PR) // PR for p in positions)) + 5
+    kp, table = build_pool(k_rows, f32, n_pages, np.random.default_rng(53))
+    vp, _ = build_pool(v_rows, f32, n_pages, np.random.default_rng(53))
+    q, kn, vn = data(5300, (n_seq, NH * HD)), data(5301, (n_seq, KVD)), data(5302, (n_seq, KVD))
+    dq, dkn, dvn = ctx.upload(q), ctx.upload(kn), ctx.upload(vn)
+    dk, dv, dtab, dpos = ctx.upload(kp), ctx.upload(vp), ctx.upload(table), ctx.upload(positions)
+    dout = ctx.empty((n_seq, NH * HD))
+    ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, groups)
+    try:
+        ctx.layer_attention_paged(dq, dkn, dvn, dk, dv, n_pages, dtab, table.shape[1], dpos, dout, n_seq, NH, NKV,
+                                  HD, max_len, 1e6)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_TARGET_GROUPS, 0)
+    got, kp_got, vp_got = dout.numpy(), dk.numpy(), dv.numpy()
+    kp_ref, vp_ref = kp.copy(), vp.copy()
+    for s, p in enumerate(positions):
+        qr, kr = oracle.rope(q[s], kn[s], NH, NKV, HD, int(p), 1e6)
+        row = table[s, p // PR] * PR + p % PR
+        kp_ref[row] = kr
+        vp_ref[row] = vn[s]
+        rows = np.array([table[s, r // PR] * PR + r % PR for r in range(p + 1)])
+        ref = oracle.attention(qr, kp_ref[rows], vp_ref[rows], NH, NKV, HD, int(p))
+        assert_close(got[s], ref, f"stream-K paged layer groups={groups} seq {s} pos {p}")
+    np.testing.assert_array_equal(kp_got, kp_ref)
+    np.testing.assert_array_equal(vp_got, vp_ref)
+    assert ctx.check_device_error() == 0
+
+
+def test_stream_k_paged_layer_bad_position(ctx):
+    """A position past the pages of the block table sets error bit 0 and leaves
+    that sequence's output and the pools untouched; the others are exact."""
+    positions = np.array([20, 40, 70], np.int32)
+    k_rows = [data(5400 + s, (int(p) + 1, KVD)) for s, p in enumerate(positions)]
+    kp, table = build_pool(k_rows, tmac_attn.TMAC_KV_F32, 12, np.random.default_rng(54))
+    table = table[:, :3]  # 48 rows per sequence: position 70 is outside
+    q, kn, vn = data(5500, (3, NH * HD)), data(5501, (3, KVD)), data(5502, (3, KVD))
+    dq, dkn, dvn, dk, dtab = ctx.upload(q), ctx.upload(kn), ctx.upload(vn), ctx.upload(kp), ctx.upload(table)
+    dpos, dout = ctx.upload(positions), ctx.upload(np.full((3, NH * HD), 7.0, np.float32))
+    ctx.layer_attention_paged(dq, dkn, dvn, dk, dk, 12, dtab, 3, dpos, dout, 3, NH, NKV, HD, 48, 1e6)
+    got = dout.numpy()
+    assert np.all(got[2] == 7.0)
+    assert ctx.check_device_error() == tmac_attn.TMAC_ERR_DEVICE_FAULT
     assert ctx.check_device_error() == 0

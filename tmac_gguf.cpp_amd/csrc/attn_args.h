@@ -58,8 +58,10 @@ struct DecodeArgs {
     const int32_t* positions;    // paged layer mode: [n_seq] position of each sequence's new token
     int max_pages;
     int n_pages;                 // pages in each pool
-    // stream-K ragged decode: per sequence (first workspace slot, slots used)
+    // stream-K ragged decode: per sequence (first workspace slot, slots used),
+    // and the launch's max_len (longer sequences give NaN and error bit 1)
     int32_t* seg_meta;
+    int sk_max_len;
 };
 
 // Chunked causal prefill: query i of sequence s sits at absolute position

@@ -778,6 +778,16 @@ __device__ __forceinline__ int64_t sk_rows(int len, int max_len) {
     return (len > 0 && len <= max_len) ? (((int64_t)len + kPageRows - 1) & ~(int64_t)(kPageRows - 1)) : 0;
 }
 
+// Rows attended by sequence s: its length, or in the layer step position + 1
+// (0 for a position outside the cache or the RoPE table, which the combine
+// reports).
+template <bool LAYER>
+__device__ __forceinline__ int sk_len(const DecodeArgs& a, int s) {
+    if (!LAYER) return a.lengths[s];
+    const int pos = a.positions[s];
+    return (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) ? 0 : pos + 1;
+}
+
 // Stream-K ragged decode.  The batch's sequences, each padded to a multiple of
 // kPageRows rows, are laid end to end in one row space of R rows, cut into
 // gridDim.x equal ranges of S = max(ceil(R / gridDim.x) rounded up to
@@ -799,7 +809,7 @@ constexpr int kSkMinRows = 64;
 // with rows, and the sequence holding row lo with its first row (s0, P0).
 // False when the row space ends before the range.  NT threads, all of which
 // must call it.
-template <int NT>
+template <int NT, bool LAYER>
 __device__ __forceinline__ bool sk_locate(const DecodeArgs& a, int64_t& S, int64_t& lo, int64_t& hi, int& last_u,
                                           int& s0, int64_t& P0) {
     constexpr int NW = NT / 64;
@@ -816,12 +826,13 @@ __device__ __forceinline__ bool sk_locate(const DecodeArgs& a, int64_t& S, int64
 #pragma unroll
     for (int r = 0; r < kKeep; ++r) {
         const int sq = r * NT + (int)threadIdx.x;
-        kept[r] = sq < a.n_seq ? sk_rows(a.lengths[sq], a.capacity) : 0;
+        kept[r] = sq < a.n_seq ? sk_rows(sk_len<LAYER>(a, sq), a.sk_max_len) : 0;
     }
     int64_t mine = 0;
 #pragma unroll
     for (int r = 0; r < kKeep; ++r) mine += kept[r];
-    for (int sq = (int)threadIdx.x + kKeep * NT; sq < a.n_seq; sq += NT) mine += sk_rows(a.lengths[sq], a.capacity);
+    for (int sq = (int)threadIdx.x + kKeep * NT; sq < a.n_seq; sq += NT)
+        mine += sk_rows(sk_len<LAYER>(a, sq), a.sk_max_len);
 #pragma unroll
     for (int mask = 1; mask < 64; mask <<= 1) mine += __shfl_xor(mine, mask);
     if (lane == 0) s_wsum[wave] = mine;
@@ -849,7 +860,7 @@ __device__ __forceinline__ bool sk_locate(const DecodeArgs& a, int64_t& S, int64
 #pragma unroll
             for (int j = 0; j < kKeep; ++j) rows = j == r ? kept[j] : rows;
         } else {
-            rows = sq < a.n_seq ? sk_rows(a.lengths[sq], a.capacity) : 0;
+            rows = sq < a.n_seq ? sk_rows(sk_len<LAYER>(a, sq), a.sk_max_len) : 0;
         }
         int64_t incl = rows;
 #pragma unroll
@@ -883,11 +894,12 @@ __device__ __forceinline__ bool sk_locate(const DecodeArgs& a, int64_t& S, int64
 // Advances (s, P) to the first sequence from s on with rows in [lo, hi)
 // (P: its first row in the row space, len: its length); false when there is
 // none.  The values are uniform, so they are kept in scalar registers.
+template <bool LAYER>
 __device__ __forceinline__ bool sk_seek(const DecodeArgs& a, int64_t lo, int64_t hi, int& s, int64_t& P, int& len) {
     for (; s < a.n_seq && P < hi; ++s) {
         s = __builtin_amdgcn_readfirstlane(s);
-        len = __builtin_amdgcn_readfirstlane(a.lengths[s]);
-        const int64_t rows = sk_rows(len, a.capacity);
+        len = __builtin_amdgcn_readfirstlane(sk_len<LAYER>(a, s));
+        const int64_t rows = sk_rows(len, a.sk_max_len);
         if (rows > 0 && lo - P < (int64_t)len) return true;  // lo - P < len: a row of s lies in [lo, hi)
         P += rows;
     }
@@ -910,18 +922,22 @@ __device__ __forceinline__ bool sk_record(const DecodeArgs& a, int s, int64_t P,
 
 // Stream-K decode, VALU group kernel (fp32 caches).  The next segment's query
 // is loaded before this one's merge, so its latency overlaps the merge.
-template <typename T, int G, int KV, int NW, int DEPTH, bool PAGED>
+// LAYER (paged layer step of a batch): sequence s attends rows 0..positions[s];
+// the segment holding row positions[s] takes the new token as the unit-grid
+// layer kernel does (RoPE of k, the cache row written, attended from registers).
+template <typename T, int G, int KV, int NW, int DEPTH, bool PAGED, bool LAYER>
 __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
     constexpr int HB = CacheFmt<T>::kHeadBytes;
     constexpr int ROWB = KV * HB;
+    constexpr int ROWF = KV * kHeadDim;  // floats per k_new / v_new row
     constexpr int NH = KV * G;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int u = blockIdx.x;
     int64_t S, lo, hi, P;
     int last_u, s, len = 0;
-    if (!sk_locate<NW * 64>(a, S, lo, hi, last_u, s, P)) return;
-    if (!sk_seek(a, lo, hi, s, P, len)) return;
+    if (!sk_locate<NW * 64, LAYER>(a, S, lo, hi, last_u, s, P)) return;
+    if (!sk_seek<LAYER>(a, lo, hi, s, P, len)) return;
 
     const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
     const int lane_row = slot / KV;
@@ -935,11 +951,16 @@ __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
     float q[G][kDimsPerLane];
     load_q(q, s);
     while (true) {
+        const int pos = len - 1;  // layer step: the new token's row
+        const float2* cs_row = LAYER ? a.rope_cs + (size_t)pos * (kHeadDim / 2) : nullptr;
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g) {
+            if (LAYER) rope8(q[g], cs_row, c);
 #pragma unroll
             for (int t = 0; t < kDimsPerLane; ++t) q[g][t] *= a.qscale;
+        }
         const int64_t r0 = max(lo - P, (int64_t)0), r1 = min(hi - P, (int64_t)len);
+        const int64_t mem_end = LAYER ? min(r1, (int64_t)pos) : r1;  // layer step: row pos comes from registers
         State<G> st;
         state_init(st);
         const size_t row0 = PAGED ? 0 : (size_t)a.offsets[s] + (size_t)r0;
@@ -947,13 +968,34 @@ __device__ __forceinline__ void decode_sk_body(const DecodeArgs& a) {
         const char* vc = reinterpret_cast<const char*>(a.v) + row0 * ROWB;
         const PageMap pm{PAGED ? a.block_table + (size_t)s * a.max_pages : nullptr, (int)r0, a.n_pages};
         unsigned bad = 0;
-        attend_rows<T, G, KV, ROWB, NW, DEPTH, PAGED>(kc, vc, (int)(r1 - r0), wave, lane_off, lane_row, lane_col, c,
-                                                     q, st, u * a.rot_mul, a.blocked != 0, pm, bad);
+        attend_rows<T, G, KV, ROWB, NW, DEPTH, PAGED>(kc, vc, (int)max(mem_end - r0, (int64_t)0), wave, lane_off,
+                                                     lane_row, lane_col, c, q, st, u * a.rot_mul, a.blocked != 0, pm,
+                                                     bad);
+        if (LAYER && r1 == len && wave == 0) {
+            // The new token: RoPE its k, write k/v to the cache row pos
+            // (tmac_gguf.cpp:1090-1091) and attend it from registers.
+            const bool mine = (lane_row == 0);
+            float kf[kDimsPerLane], vf[kDimsPerLane];
+            if (mine) {
+                const size_t in = (size_t)s * ROWF + kvh * kHeadDim + 4 * c;
+                load8(kf, a.k_new + in);
+                load8(vf, a.v_new + in);
+                rope8(kf, cs_row, c);
+                size_t row = (size_t)pos;
+                if (PAGED) row = (size_t)page_of(pm, pos, bad) * kPageRows + (pos & (kPageRows - 1));
+                put_row<T>(kf, reinterpret_cast<char*>(a.k_out) + row * ROWB + lane_col, c, true);
+                put_row<T>(vf, reinterpret_cast<char*>(a.v_out) + row * ROWB + lane_col, c, true);
+            } else {
+#pragma unroll
+                for (int t = 0; t < kDimsPerLane; ++t) kf[t] = vf[t] = 0.f;
+            }
+            attend<G, KV, true>(q, st, kf, vf, mine);
+        }
         if (PAGED && bad && lane == 0) atomicOr(a.err, 4);
         const bool direct = sk_record(a, s, P, len, S, last_u);
         int s2 = s + 1, len2 = 0;
-        int64_t P2 = P + sk_rows(len, a.capacity);
-        const bool more = sk_seek(a, lo, hi, s2, P2, len2);
+        int64_t P2 = P + sk_rows(len, a.sk_max_len);
+        const bool more = sk_seek<LAYER>(a, lo, hi, s2, P2, len2);
         if (more) load_q(q, s2);
         float* ws_slot = direct ? nullptr : a.ws + (size_t)(u + s) * NH * kPartialStride;
         finish<G, KV, NW>(st, lane, wave, direct, a.out + (size_t)s * NH * kHeadDim, ws_slot);
@@ -1176,18 +1218,29 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
 // Combine of the stream-K ragged decode: one wave per (head, sequence).  It
 // also writes the outputs of the sequences the decode kernel skips: zeros for
 // an empty sequence, NaN (and error bit 1) for one longer than max_len.
-template <int G, int KV>
+// LAYER: a position outside the cache or the RoPE table sets error bit 0 and
+// leaves the output as it was (as the unit-grid layer kernel does).
+template <int G, int KV, bool LAYER>
 __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
     constexpr int NH = KV * G;
     constexpr int SP = NH * kPartialStride;
     const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
-    const int len = a.lengths[seq];
+    int len;
+    if (LAYER) {
+        len = sk_len<true>(a, seq);
+        if (len == 0) {
+            if (h == 0 && d == 0) atomicOr(a.err, 1);
+            return;
+        }
+    } else {
+        len = a.lengths[seq];
+    }
     float* o = a.out + ((size_t)seq * NH + h) * kHeadDim + d;
     if (len <= 0) {
         *o = 0.f;
         return;
     }
-    if (len > a.capacity) {
+    if (len > a.sk_max_len) {
         *o = __builtin_nanf("");
         if (h == 0 && d == 0) atomicOr(a.err, 2);
         return;
@@ -1224,10 +1277,10 @@ __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
 // Stream-K ragged decode (fp32 caches) and its combine.
 #define TMAC_SK_KERNELS(G, KV)                                                                     \
     extern "C" __global__ __launch_bounds__(256) void tmac_decode_sk_g##G##_kv##KV(DecodeArgs a) {  \
-        decode_sk_body<float, G, KV, 4, kPrefetchDepth, false>(a);                                 \
+        decode_sk_body<float, G, KV, 4, kPrefetchDepth, false, false>(a);                          \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(64) void tmac_decode_sk_combine_g##G##_kv##KV(DecodeArgs a) { \
-        combine_sk_body<G, KV>(a);                                                                 \
+        combine_sk_body<G, KV, false>(a);                                                          \
     }
 
 // Narrow caches (bf16, fp16, Q8_0): the default group (8 waves) and head
@@ -1283,7 +1336,13 @@ __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
     TMAC_PAGED_KERNELS(G, KV, f16, _Float16, kPrefetchDepth16)                          \
     TMAC_PAGED_KERNELS(G, KV, q8, q8_0_t, kPrefetchDepthQ8)                             \
     extern "C" __global__ __launch_bounds__(256) void tmac_decode_sk_p_f32_g##G##_kv##KV(DecodeArgs a) { \
-        decode_sk_body<float, G, KV, 4, kPrefetchDepth, true>(a);                       \
+        decode_sk_body<float, G, KV, 4, kPrefetchDepth, true, false>(a);                \
+    }                                                                                   \
+    extern "C" __global__ __launch_bounds__(256) void tmac_layer_sk_p_f32_g##G##_kv##KV(DecodeArgs a) { \
+        decode_sk_body<float, G, KV, 4, kPrefetchDepth, true, true>(a);                 \
+    }                                                                                   \
+    extern "C" __global__ __launch_bounds__(64) void tmac_layer_sk_combine_g##G##_kv##KV(DecodeArgs a) { \
+        combine_sk_body<G, KV, true>(a);                                                \
     }                                                                                   \
     extern "C" __global__ __launch_bounds__(64) void tmac_decode_p_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, kPaged>(a);                                                 \
@@ -2366,8 +2425,8 @@ __device__ __forceinline__ void mdecode_sk_body(const DecodeArgs& a) {
     constexpr int NH = KV * G;
     int64_t S, lo, hi, P;
     int last_u, s, len = 0;
-    if (!sk_locate<kMWaves * 64>(a, S, lo, hi, last_u, s, P)) return;
-    for (bool first = true; sk_seek(a, lo, hi, s, P, len); ++s, first = false) {
+    if (!sk_locate<kMWaves * 64, false>(a, S, lo, hi, last_u, s, P)) return;
+    for (bool first = true; sk_seek<false>(a, lo, hi, s, P, len); ++s, first = false) {
         if (!first) __syncthreads();  // the previous segment's merge reads the LDS this one's tiles reuse
         const int64_t r0 = max(lo - P, (int64_t)0), r1 = min(hi - P, (int64_t)len);
         const bool direct = sk_record(a, s, P, len, S, last_u);
@@ -2375,7 +2434,7 @@ __device__ __forceinline__ void mdecode_sk_body(const DecodeArgs& a) {
         mdecode_segment<T, G, KV, PAGED ? kPaged : kRagged>(a, s, 0, 1, 0, PAGED ? 0 : (size_t)a.offsets[s],
                                                             (int)r0, (int)(r1 - r0),
                                                             a.out + (size_t)s * NH * kHeadDim, ws_slot);
-        P += sk_rows(len, a.capacity);
+        P += sk_rows(len, a.sk_max_len);
     }
 }
 

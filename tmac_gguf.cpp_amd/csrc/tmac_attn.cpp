@@ -109,6 +109,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> combine_p[2];  // split merge of the paged modes
     std::map<std::pair<int, int>, hipFunction_t> decode_sk, combine_sk;  // stream-K ragged decode (fp32)
     std::map<std::pair<int, int>, hipFunction_t> decode_sk_p;             // the same over paged caches
+    std::map<std::pair<int, int>, hipFunction_t> layer_sk_p, combine_sk_l;  // stream-K paged layer step (fp32)
     std::map<std::pair<int, int>, hipFunction_t> mdecode_sk[kNarrowTypes][2];  // MFMA stream-K: ragged, paged
     // MFMA decode (bf16, fp16, Q8_0): uniform, ragged, paged, layer, paged layer
     std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
@@ -439,7 +440,12 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
 // so only the many-sequence case gains: bf16 3000 x 40 144 -> 105, Q8_0
 // 154 -> 120; but bf16 384 x 2048 53 -> 64, 1024 x 512 54 -> 81, 2048 x 512
 // 119 -> 124, Q8_0 1024 x 512 61 -> 81.
-enum SkKind { kSkF32Ragged, kSkF32Paged, kSkMfma };
+// Paged layer step (fp32): the unit grid has no row-count hint there and
+// sizes its splits from max_len, so stream-K wins from few sequences on:
+// positions U[0, L): 16 x 32768 56.8 -> 49.8, 64 x 16384 106 -> 89,
+// 128 x 8192 109 -> 98, 256 x 4096 113 -> 107, 384 x 2048 99 -> 92,
+// 3000 x 40 184 -> 97; but 1024 x 512 82 -> 90.
+enum SkKind { kSkF32Ragged, kSkF32Paged, kSkF32Layer, kSkMfma };
 bool use_stream_k(const tmac_context* ctx, int n_seq, SkKind kind) {
     if (ctx->opt_stream_k == 0) return false;
     if (ctx->opt_stream_k == 2) return true;
@@ -447,6 +453,7 @@ bool use_stream_k(const tmac_context* ctx, int n_seq, SkKind kind) {
     if (kind == kSkF32Paged) return n2 >= ctx->n_cu;
     const bool many = n_seq > 10 * ctx->n_cu;
     if (kind == kSkMfma) return many;
+    if (kind == kSkF32Layer) return n_seq <= 2 * ctx->n_cu || many;
     return (n2 >= ctx->n_cu && n2 <= 3 * (int64_t)ctx->n_cu) || many;
 }
 
@@ -481,7 +488,7 @@ int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, unsig
     a.rot_mul = (int)ctx->opt_rot_mul;
     a.blocked = (int)ctx->opt_blocked;
     a.err = ctx->err;
-    a.capacity = max_len;
+    a.sk_max_len = max_len;
     if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
     if (max_len > INT_MAX - kPageRows) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: max_len too large");
     // One workgroup per CU; two when the sequences outnumber the CUs (more
@@ -607,6 +614,15 @@ int tmac_init(tmac_context** out, int device) {
                     if ((e = get_function(ctx, &f, name)) != hipSuccess)
                         return bail(hip_fail(ctx, e, name));
                     ctx->decode_sk_p[{sh[0], sh[1]}] = f;
+                } else {
+                    std::snprintf(name, sizeof(name), "tmac_layer_sk_p_f32_g%d_kv%d", sh[0], sh[1]);
+                    if ((e = get_function(ctx, &f, name)) != hipSuccess)
+                        return bail(hip_fail(ctx, e, name));
+                    ctx->layer_sk_p[{sh[0], sh[1]}] = f;
+                    std::snprintf(name, sizeof(name), "tmac_layer_sk_combine_g%d_kv%d", sh[0], sh[1]);
+                    if ((e = get_function(ctx, &f, name)) != hipSuccess)
+                        return bail(hip_fail(ctx, e, name));
+                    ctx->combine_sk_l[{sh[0], sh[1]}] = f;
                 }
                 std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", pp, sh[0], sh[1]);
                 if ((e = get_function(ctx, &f, name)) != hipSuccess)
@@ -963,6 +979,11 @@ int tmac_layer_attention_paged(tmac_context* ctx, tmac_stream stream, int kv_dty
     a.block_table = block_table;
     a.max_pages = max_pages;
     a.n_pages = n_pages;
+    if (kv_dtype == TMAC_KV_F32 && ctx->opt_split_len == 0 && use_stream_k(ctx, n_seq, kSkF32Layer)) {
+        const std::pair<int, int> key{n_head / n_kv_head, n_kv_head};
+        return run_decode_sk(ctx, (hipStream_t)stream, ctx->layer_sk_p.at(key), 256, ctx->combine_sk_l.at(key), a,
+                             n_seq, max_len);
+    }
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, max_len, n_kv_head);
 }
 
