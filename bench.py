@@ -309,6 +309,37 @@ def bench_c4(ctx, stream, steps, warmup, n_seq=16, max_len=32768):
             "gbs": nbytes / (mean_ms * 1e-3) / 1e9, "pct_of_peak": nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS * 100}
 
 
+def bench_layer_paged(ctx, stream, steps, warmup, n_seq=64, max_pos=16384):
+    """Batched paged layer step (fp32): n_seq sequences at positions U[0, max_pos), 16-row pages in random pool
+    order; RoPE + cache-row write + attention over rows 0..pos of each sequence."""
+    rng = np.random.default_rng(12)
+    pos = np.floor(rng.random(n_seq) * max_pos).astype(np.int32)
+    need = pos // 16 + 1
+    n_pages, max_pages = int(need.sum()), int(need.max())
+    table = np.zeros((n_seq, max_pages), np.int32)
+    perm = rng.permutation(n_pages).astype(np.int32)
+    first = np.concatenate([[0], np.cumsum(need[:-1])])
+    for i in range(n_seq):
+        table[i, :need[i]] = perm[first[i]:first[i] + need[i]]
+    dk = ctx.upload(rng.standard_normal((n_pages * 16, KVD), dtype=np.float32))
+    dv = ctx.upload(rng.standard_normal((n_pages * 16, KVD), dtype=np.float32))
+    dq = ctx.upload(rng.standard_normal((n_seq, NH * HD), dtype=np.float32))
+    dkn = ctx.upload(rng.standard_normal((n_seq, KVD), dtype=np.float32))
+    dvn = ctx.upload(rng.standard_normal((n_seq, KVD), dtype=np.float32))
+    dtab, dpos, dout = ctx.upload(table), ctx.upload(pos), ctx.empty((n_seq, NH * HD))
+
+    def launch():
+        ctx.layer_attention_paged(dq, dkn, dvn, dk, dv, n_pages, dtab, max_pages, dpos, dout, n_seq, NH, NKV, HD,
+                                  max_pages * 16, 1e6, stream=stream)
+
+    per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
+    nbytes = algo_bytes(pos + 1)
+    for d in (dk, dv, dq, dkn, dvn, dtab, dpos, dout):
+        d.free()
+    return {"rows_total": int((pos + 1).sum()), "bytes": nbytes, "mean_us": mean_ms * 1e3,
+            "gbs": nbytes / (mean_ms * 1e-3) / 1e9}
+
+
 C5_FLOPS = 13_157_007_360  # 4 seqs x 14 heads x sum_{i<512} (1537 + i) rows x 4*64 flop (QK^T + PV)
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
@@ -482,7 +513,7 @@ def main():
     ap.add_argument("--sections", default="c1,c2,c4,c5,qkv,kv,paged,ragged",
                     help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv,kv (bf16, "
                          "fp16, Q8_0 caches), kv16 (bf16, fp16 only), paged, ragged (256 sequences of "
-                         "U[1, 4096] rows, both fp32 ragged schedules)")
+                         "U[1, 4096] rows and a 64-sequence paged layer step, both fp32 schedules)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -537,6 +568,15 @@ def main():
         ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 1)
         extra["ragged_256"] = r
         log(f"[bench] ragged 256 x U[1,4096]: stream-K {r['stream_k']['mean_us']:.1f} us "
+            f"({r['stream_k']['gbs']:.0f} GB/s), unit grid {r['unit_grid']['mean_us']:.1f} us "
+            f"({r['unit_grid']['gbs']:.0f} GB/s)")
+        r = {}
+        for name, sk in (("stream_k", 2), ("unit_grid", 0)):
+            ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, sk)
+            r[name] = bench_layer_paged(ctx, stream, max(10, args.steps // 2), args.warmup)
+        ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 1)
+        extra["layer_paged_64"] = r
+        log(f"[bench] paged layer step 64 x U[0,16384): stream-K {r['stream_k']['mean_us']:.1f} us "
             f"({r['stream_k']['gbs']:.0f} GB/s), unit grid {r['unit_grid']['mean_us']:.1f} us "
             f"({r['unit_grid']['gbs']:.0f} GB/s)")
     for tn in ("bf16", "f16", "q8"):
