@@ -421,7 +421,9 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     return launch(ctx, k.combine, (unsigned)a.n_head, (unsigned)n_seq, 64, stream, &a);
 }
 
-// Schedule of the fp32 ragged decode.  Stream-K (below) pays a pipeline
+// Schedule of the ragged and paged decode and of the paged layer step: the
+// unit grid (run_decode) or stream-K (run_decode_sk).
+// fp32 ragged decode: stream-K pays a pipeline
 // restart and a merge at every sequence change inside a range, so it wins
 // while ranges hold few sequences, and again at many sequences, where the
 // unit grid's serial scan of the lengths dominates.  Measured with lengths
@@ -476,12 +478,14 @@ hipFunction_t stream_k_kernel(const tmac_context* ctx, int dt, bool paged, int n
     return it->second;
 }
 
-// Stream-K ragged decode (fp32 caches): the kernel cuts the batch's padded
-// row space into `units` equal ranges (one workgroup each, one per CU by
-// default), sized from the lengths on the device, so the total_rows hint is
-// not needed and graph replays may change the lengths.  The combine launch
-// always follows: it merges the sequences spread over several workgroups and
-// writes the outputs of empty and over-long ones.
+// Stream-K launch (ragged or paged decode on any cache type, fp32 paged
+// layer step): the kernel cuts the batch's padded row space into `units`
+// equal ranges (one workgroup each, one per CU by default), sized from the
+// lengths or positions on the device, so the total_rows hint is not needed
+// and graph replays may change them.  The workspace holds units + n_seq
+// partial slots whatever the lengths.  The combine launch always follows: it
+// merges the sequences spread over several workgroups and writes the outputs
+// of empty and over-long ones.
 int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, unsigned threads, hipFunction_t combine,
                   DecodeArgs& a, int n_seq, int max_len) {
     a.qscale = kQScale;
@@ -490,7 +494,7 @@ int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, unsig
     a.err = ctx->err;
     a.sk_max_len = max_len;
     if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
-    if (max_len > INT_MAX - kPageRows) return fail(ctx, TMAC_ERR_INVALID_ARG, "decode_ragged: max_len too large");
+    if (max_len > INT_MAX - kPageRows) return fail(ctx, TMAC_ERR_INVALID_ARG, "stream-K decode: max_len too large");
     // One workgroup per CU; two when the sequences outnumber the CUs (more
     // sequence changes per range, whose stalls the second workgroup covers).
     const int64_t auto_units = (int64_t)ctx->n_cu * (n_seq > ctx->n_cu ? 2 : 1);
