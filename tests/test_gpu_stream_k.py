@@ -345,3 +345,22 @@ def test_stream_k_paged_layer_bad_position(ctx):
     assert np.all(got[2] == 7.0)
     assert ctx.check_device_error() == tmac_attn.TMAC_ERR_DEVICE_FAULT
     assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_stream_k_twenty_thousand_sequences(ctx, paged):
+    """20,000 sequences of 0..12 rows: the row total and the range search run
+    over 79 rounds of 256 lengths in every workgroup."""
+    rng = np.random.default_rng(56)
+    lens = rng.integers(0, 13, 20000).astype(np.int32)
+    lens, offs, total, k, v, q = ragged_batch(ctx, 5600, lens)
+    ref = reference(q, k, v, offs, lens)
+    dq, dlen, dout = ctx.upload(q), ctx.upload(lens), ctx.empty((lens.size, NH * HD))
+    if paged:
+        kp, vp, table, n_pages = to_pages(k, v, offs, lens, rng)
+        ctx.decode_paged(dq, ctx.upload(kp), ctx.upload(vp), n_pages, ctx.upload(table), table.shape[1], dlen, dout,
+                         lens.size, NH, NKV, HD, 12)
+    else:
+        ctx.decode_ragged(dq, ctx.upload(k), ctx.upload(v), ctx.upload(offs), dlen, dout, lens.size, NH, NKV, HD, 12)
+    assert_close(dout.numpy(), ref, f"20,000 sequences paged={paged}")
+    assert ctx.check_device_error() == 0

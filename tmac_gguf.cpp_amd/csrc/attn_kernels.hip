@@ -831,6 +831,7 @@ __device__ __forceinline__ bool sk_locate(const DecodeArgs& a, int64_t& S, int64
     int64_t mine = 0;
 #pragma unroll
     for (int r = 0; r < kKeep; ++r) mine += kept[r];
+#pragma unroll 8
     for (int sq = (int)threadIdx.x + kKeep * NT; sq < a.n_seq; sq += NT)
         mine += sk_rows(sk_len<LAYER>(a, sq), a.sk_max_len);
 #pragma unroll

@@ -430,7 +430,10 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
 // uniform in 1..L (unit grid -> stream-K, us): 128 x 8192: 108 -> 93;
 // 256 x 4096: 107 -> 96; 384 x 2048: 97 -> 81; 1024 x 512: 63 -> 83;
 // 1536 x 1024: 148 -> 160; 2048 x 1024: 198 -> 214; 3000 x 40: 180 -> 85;
-// 4096 x 256: 194 -> 178.  Fewer sequences split well on the unit grid:
+// 4096 x 256: 194 -> 178; 20000 x U[0, 12]: 3700 -> 350; 60000 x U[0, 12]:
+// 29600 -> 1062 (every unit-grid workgroup scans the lengths up to its
+// unit, so that grid's cost grows with the square of the sequence count).
+// Fewer sequences split well on the unit grid:
 // 16 x 32768 59.1 -> 59.6, 64 x 16384 95.6 -> 96.7, 256 x 4096 equal
 // lengths 159.1 -> 160.4.
 // Paged caches (the unit grid there runs 8-wave workgroups): stream-K wins
