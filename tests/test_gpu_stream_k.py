@@ -364,3 +364,40 @@ def test_stream_k_twenty_thousand_sequences(ctx, paged):
         ctx.decode_ragged(dq, ctx.upload(k), ctx.upload(v), ctx.upload(offs), dlen, dout, lens.size, NH, NKV, HD, 12)
     assert_close(dout.numpy(), ref, f"20,000 sequences paged={paged}")
     assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("dt", [tmac_attn.TMAC_KV_BF16, tmac_attn.TMAC_KV_Q8_0])
+def test_stream_k_mfma_graph_replay(ctx, dt):
+    """A captured MFMA stream-K decode (bf16 / Q8_0 ragged) replayed after the
+    device-side lengths and the queries change; every replay against the
+    oracle over the cache's widened rows."""
+    max_len, n_seq = 3000, 20
+    kb = store(data(5700 + dt, (n_seq * max_len, KVD), 2), dt)
+    vb = store(data(5710 + dt, (n_seq * max_len, KVD), 2), dt)
+    kw, vw = widen(kb, dt), widen(vb, dt)
+    offs = np.arange(n_seq, dtype=np.int64) * max_len
+    dk, dv, doff = ctx.upload(kb), ctx.upload(vb), ctx.upload(offs)
+    dq, dlen, dout = ctx.empty((n_seq, NH * HD)), ctx.empty(n_seq, np.int32), ctx.empty((n_seq, NH * HD))
+    s = ctx.stream()
+    rng = np.random.default_rng(57)
+    try:
+        dlen.copy_from(np.ones(n_seq, np.int32))
+        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, n_seq, NH, NKV, HD, max_len, stream=s, kv_dtype=dt)
+        ctx.synchronize(s)
+        ctx.step_begin(s)
+        ctx.decode_ragged(dq, dk, dv, doff, dlen, dout, n_seq, NH, NKV, HD, max_len, stream=s, kv_dtype=dt)
+        g = ctx.step_end(s)
+        try:
+            for rep in range(3):
+                lens = rng.integers(0, max_len + 1, n_seq).astype(np.int32)
+                q = data(5720 + rep, (n_seq, NH * HD))
+                dq.copy_from(q)
+                dlen.copy_from(lens)
+                ctx.graph_launch(g, s)
+                ctx.synchronize(s)
+                assert_close(dout.numpy(), reference(q, kw, vw, offs, lens), f"dt={dt} replay {rep}")
+        finally:
+            ctx.graph_destroy(g)
+    finally:
+        ctx.destroy_stream(s)
+    assert ctx.check_device_error() == 0
