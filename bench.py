@@ -34,6 +34,7 @@ PKG = os.path.join(REPO, "tmac_gguf.cpp_amd")
 sys.path.insert(0, PKG)
 
 import tmac_attn  # noqa: E402
+import workloads  # noqa: E402
 
 METRIC = "decode-attn achieved HBM GB/s (% of peak) + µs/call at Qwen2-0.5B shape"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
@@ -90,10 +91,7 @@ def pct(a, p):
 
 def bench_c3(ctx, stream, steps, warmup, n_seq=256, n_pos=4096):
     log(f"[bench] C3: generating {n_seq}x{n_pos} fp32 K/V ({n_seq * n_pos * ROW_BYTES / 1e9:.2f} GB)")
-    rng = np.random.default_rng(3)
-    q = rng.standard_normal((n_seq, NH * HD), dtype=np.float32)
-    k = rng.standard_normal((n_seq * n_pos, KVD), dtype=np.float32)
-    v = rng.standard_normal((n_seq * n_pos, KVD), dtype=np.float32)
+    q, k, v = workloads.c3(n_seq, n_pos)
     dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     dout = ctx.empty((n_seq, NH * HD))
     split_len, n_splits = ctx.query_split(n_seq, n_pos, NH, NKV)
@@ -123,18 +121,18 @@ KV_TYPES = {"f32": 0, "bf16": 1, "f16": 2, "q8": 3}  # tmac_kv_dtype
 ROW_BYTES_BY_TYPE = {"f32": KVD * 4, "bf16": KVD * 2, "f16": KVD * 2, "q8": NKV * 68}
 
 
-def _narrow_cache(ctx, rng, dtype_name, rows):
-    """`rows` cache rows of N(0,1) values in the named element type, converted
-    on the device (tmac_kv_convert) from fp32 drawn as in config 3."""
-    import tmac_attn
+def _narrow_cache(ctx, host, dtype_name):
+    """The fp32 cache rows `host` in the named element type, converted on the
+    device (tmac_kv_convert)."""
     dt = KV_TYPES[dtype_name]
     if dt == 0:
-        return ctx.upload(rng.standard_normal((rows, KVD), dtype=np.float32))
+        return ctx.upload(host)
+    rows = host.shape[0]
     dst = ctx.empty(rows * ROW_BYTES_BY_TYPE[dtype_name], np.uint8)
     chunk = 1 << 20  # rows per conversion (bounded staging buffer)
     for r0 in range(0, rows, chunk):
         n = min(chunk, rows - r0)
-        tmp = ctx.upload(rng.standard_normal((n, KVD), dtype=np.float32))
+        tmp = ctx.upload(host[r0:r0 + n])
         ctx.kv_convert(dt, tmp, dst.at(r0 * ROW_BYTES_BY_TYPE[dtype_name]), n * KVD)
         ctx.synchronize()
         tmp.free()
@@ -145,10 +143,10 @@ def bench_kvn(ctx, stream, steps, warmup, dtype_name, n_seq=256, n_pos=4096):
     """Config 3's workload on a narrow cache (tmac_attention_decode_batched_kv):
     the same rows, bf16/fp16 half the bytes, Q8_0 0.27x."""
     dt = KV_TYPES[dtype_name]
-    rng = np.random.default_rng(3)
-    q = rng.standard_normal((n_seq, NH * HD), dtype=np.float32)
+    q, k, v = workloads.c3(n_seq, n_pos)
     dq, dout = ctx.upload(q), ctx.empty((n_seq, NH * HD))
-    dk, dv = _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos), _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos)
+    dk, dv = _narrow_cache(ctx, k, dtype_name), _narrow_cache(ctx, v, dtype_name)
+    del k, v
 
     def launch():
         ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, stream=stream, kv_dtype=dt)
@@ -172,9 +170,10 @@ def bench_paged(ctx, stream, steps, warmup, dtype_name, n_seq=256, n_pos=4096):
     n_pages = n_seq * n_pos // page_rows
     table = rng.permutation(n_pages).astype(np.int32).reshape(n_seq, n_pos // page_rows)
     lens = np.full(n_seq, n_pos, np.int32)
-    q = rng.standard_normal((n_seq, NH * HD), dtype=np.float32)
+    q, k, v = workloads.c3(n_seq, n_pos)  # pool page p holds config-3 rows 16p..16p+15
     dq, dout, dtab, dlen = ctx.upload(q), ctx.empty((n_seq, NH * HD)), ctx.upload(table), ctx.upload(lens)
-    dk, dv = _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos), _narrow_cache(ctx, rng, dtype_name, n_seq * n_pos)
+    dk, dv = _narrow_cache(ctx, k, dtype_name), _narrow_cache(ctx, v, dtype_name)
+    del k, v
 
     def launch():
         ctx.decode_paged(dq, dk, dv, n_pages, dtab, table.shape[1], dlen, dout, n_seq, NH, NKV, HD, n_pos,
@@ -190,10 +189,7 @@ def bench_paged(ctx, stream, steps, warmup, dtype_name, n_seq=256, n_pos=4096):
 
 
 def bench_c1(ctx, stream, steps=200, warmup=20):
-    rng = np.random.default_rng(1)
-    q = rng.standard_normal(NH * HD, dtype=np.float32)
-    k = rng.standard_normal((256, KVD), dtype=np.float32)
-    v = rng.standard_normal((256, KVD), dtype=np.float32)
+    q, k, v = workloads.c1()
     dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     dout = ctx.empty(NH * HD)
 
@@ -211,14 +207,12 @@ def bench_c1(ctx, stream, steps=200, warmup=20):
 def bench_c2(ctx, stream, layers=24, cap=256, use_graph=True):
     """24-layer step graph (one fused launch per layer + a position advance),
     replayed for positions 0..cap-1; every replay timed with events."""
-    rng = np.random.default_rng(2)
     kc = ctx.empty((layers, cap, KVD))
     vc = ctx.empty((layers, cap, KVD))
     kc.fill_bytes(0, stream)
     vc.fill_bytes(0, stream)
-    dq = ctx.upload(rng.standard_normal((layers, NH * HD), dtype=np.float32))
-    dkn = ctx.upload(rng.standard_normal((layers, KVD), dtype=np.float32))
-    dvn = ctx.upload(rng.standard_normal((layers, KVD), dtype=np.float32))
+    q0, kn0, vn0 = workloads.c2(layers, 1)  # the first step's inputs (the timing does not depend on them)
+    dq, dkn, dvn = ctx.upload(q0[0]), ctx.upload(kn0[0]), ctx.upload(vn0[0])
     dout = ctx.empty((layers, NH * HD))
     pos = ctx.upload(np.zeros(1, np.int32))
     ctx.rope_prepare(HD, 1e6, cap)
@@ -285,14 +279,8 @@ def c2_graph(ctx, stream, layer, pos, layers, cap):
 
 
 def bench_c4(ctx, stream, steps, warmup, n_seq=16, max_len=32768):
-    rng = np.random.default_rng(4)
-    u = rng.random(n_seq)
-    lens = (1 + np.floor(u * max_len)).astype(np.int32)
-    offs = np.concatenate([[0], np.cumsum(lens[:-1], dtype=np.int64)]).astype(np.int64)
+    q, k, v, offs, lens = workloads.c4(n_seq, max_len)
     total = int(lens.sum())
-    q = rng.standard_normal((n_seq, NH * HD), dtype=np.float32)
-    k = rng.standard_normal((total, KVD), dtype=np.float32)
-    v = rng.standard_normal((total, KVD), dtype=np.float32)
     dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     doff, dlen = ctx.upload(offs), ctx.upload(lens)
     dout = ctx.empty((n_seq, NH * HD))
@@ -414,10 +402,7 @@ def bench_qkv(ctx, stream, steps, warmup, layers=24, sets=16):
 def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
     """Config 5: chunked causal prefill on bf16 MFMA."""
     cap = prefix + n_q
-    rng = np.random.default_rng(5)
-    q = rng.standard_normal((n_seq, n_q, NH * HD), dtype=np.float32)
-    k = rng.standard_normal((n_seq, cap, KVD), dtype=np.float32)
-    v = rng.standard_normal((n_seq, cap, KVD), dtype=np.float32)
+    q, k, v = workloads.c5(n_seq, n_q, prefix)
     dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     dout = ctx.empty((n_seq, n_q, NH * HD))
 
@@ -433,11 +418,45 @@ def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
             "bytes": n_seq * n_q * NH * HD * 4 * 2 + n_seq * cap * KVD * 4 * 2}
 
 
-def cpu_baseline(c3_data, budget_s: float = 10.0):
+def _cpu_facts():
+    """The host CPU as /proc/cpuinfo names it, and the CPUs this process may run on."""
+    facts = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key in ("model name", "vendor_id", "cpu family", "model", "stepping", "cpu MHz") and \
+                        key not in facts:
+                    facts[key] = val.strip()
+                if not line.strip() and facts:
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return facts, usable
+
+
+def _median_of(fn, reps: int):
+    """One untimed warm-up call, then `reps` timed calls; returns (median s, all times, last result)."""
+    fn()
+    times, res = [], None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        res = fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), times, res
+
+
+def cpu_baseline(c3_data, budget_s: float = 12.0, reps: int = 5):
     """The reference CPU attention path (oracle/, -O3 build, one thread) timed
-    on a sample of the config-3 batch; the same sequences' GPU outputs are
-    checked against it.  Test infrastructure: the oracle is the checker here,
-    never the measured product."""
+    on a sample of the config-3 batch (1 warm-up + `reps` timed runs, median);
+    the same sequences' GPU outputs are checked against the parity build.
+    Test infrastructure: the oracle is the checker here, never the measured
+    product."""
     sys.path.insert(0, REPO)
     import oracle  # noqa: E402  (only this leg may import it)
 
@@ -447,52 +466,49 @@ def cpu_baseline(c3_data, budget_s: float = 10.0):
     t0 = time.perf_counter()
     oracle.attention_ragged(q[:1], k, v, offs[:1], lens[:1], NH, NKV, HD, n_threads=1, timing=True)
     t1 = time.perf_counter() - t0
-    n = int(max(1, min(n_seq, (budget_s / 3) / max(t1, 1e-6))))
-    times = []
-    ref = None
-    while len(times) < 3 and (sum(times) < budget_s or len(times) < 1):
-        t0 = time.perf_counter()
-        ref = oracle.attention_ragged(q[:n], k, v, offs[:n], lens[:n], NH, NKV, HD, n_threads=1, timing=True)
-        times.append(time.perf_counter() - t0)
-    sec = float(np.median(times))
+    # sample size: (reps + 1) single-thread runs within the budget
+    n = int(max(1, min(n_seq, budget_s / (reps + 1) / max(t1, 1e-6))))
+
+    def single():
+        return oracle.attention_ragged(q[:n], k, v, offs[:n], lens[:n], NH, NKV, HD, n_threads=1, timing=True)
+
+    sec, times, _ = _median_of(single, reps)
     nbytes = algo_bytes(lens[:n])
+    facts, usable = _cpu_facts()
     # the same restatement spread over (sequence, head) on the host cores this job may use
-    n_thr = min(16, os.cpu_count() or 1)
+    n_thr = max(1, min(16, usable))
     n_mt = int(min(n_seq, max(n, n * n_thr)))
-    mt = []
-    while len(mt) < 3:
-        t0 = time.perf_counter()
-        oracle.attention_ragged(q[:n_mt], k, v, offs[:n_mt], lens[:n_mt], NH, NKV, HD, n_threads=n_thr,
-                                timing=True)
-        mt.append(time.perf_counter() - t0)
-    sec_mt = float(np.median(mt))
-    # checker: parity build (-ffp-contract=off) on the sampled sequences
-    chk = oracle.attention_ragged(q[:n], k, v, offs[:n], lens[:n], NH, NKV, HD,
-                                  n_threads=min(16, os.cpu_count() or 1))
-    err = np.abs(gpu_out[:n].astype(np.float64) - chk)
+
+    def multi():
+        return oracle.attention_ragged(q[:n_mt], k, v, offs[:n_mt], lens[:n_mt], NH, NKV, HD, n_threads=n_thr,
+                                       timing=True)
+
+    sec_mt, mt, _ = _median_of(multi, reps)
+    # checker: parity build (-ffp-contract=off) on every config-3 sequence
+    chk = oracle.attention_ragged(q, k, v, offs, lens, NH, NKV, HD, n_threads=n_thr)
+    err = np.abs(gpu_out.astype(np.float64) - chk)
     tol = 2e-5 + 1e-4 * np.abs(chk)
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {
         "value": nbytes / sec / 1e9,
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
         "sample": f"{n} of {n_seq} config-3 sequences ({n_pos} rows each, {nbytes} algorithmic bytes), "
-                  f"median of {len(times)} runs, oracle -O3 single thread",
+                  f"median of {reps} timed runs after 1 warm-up, oracle timing build on one thread",
+        "reps": reps,
+        "warmup": 1,
+        "run_s": [round(t, 4) for t in times],
         "us_per_seq": sec / n * 1e6,
+        "flags": oracle.BUILD_FLAGS,
         "all_cores": {"value": algo_bytes(lens[:n_mt]) / sec_mt / 1e9, "unit": "GB/s", "cores": n_thr,
-                      "sample": f"{n_mt} sequences, median of {len(mt)} runs, OpenMP over (sequence, head)"},
-        "cpu_model": cpu_model,
+                      "sample": f"{n_mt} sequences, median of {reps} timed runs after 1 warm-up, OpenMP over "
+                                f"(sequence, head)",
+                      "run_s": [round(t, 4) for t in mt]},
+        "cpu_model": facts.get("model name", ""),
+        "cpuinfo": facts,
+        "nproc": usable,
         "host_threads": os.cpu_count(),
-    }, {"sequences_checked": n, "max_abs_err": float(err.max()), "pass": bool(np.all(err <= tol))}
+    }, {"sequences_checked": n_seq, "max_abs_err": float(err.max()), "pass": bool(np.all(err <= tol))}
 
 
 def main():
@@ -627,7 +643,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: N(0,1) fp32 q/k/v from numpy PCG64 seed 3, resident in HBM",
+        "data": "synthetic: N(0,1) fp32 q/k/v from seeded splitmix64 -> xoshiro256** -> Box-Muller streams "
+                "(tmac_synth_normal): sequence s draws q, K, V from streams ((3*16+t) << 32) + s, t = 0, 1, 2; "
+                "resident in HBM",
         "config": {
             "workload": "config 3: batched decode, 256 seqs x 4096-row fp32 KV cache "
                         "(row = [2 kv heads][64]), 14 q heads, head_dim 64, GQA 7, one query each",

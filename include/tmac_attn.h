@@ -358,7 +358,14 @@ int tmac_check_device_error(tmac_context* ctx);
 int tmac_step_begin(tmac_context* ctx, tmac_stream stream);
 /* Ends capture.  *graph == NULL: instantiates a new executable graph.
  * *graph != NULL: updates it in place (hipGraphExecUpdate) and re-instantiates
- * only if the topology changed. */
+ * only if the topology changed.
+ * A graph keeps the addresses of the context's split-KV workspace and RoPE
+ * tables that its captured launches used.  While any graph of the context is
+ * alive, an eager call that needs a larger workspace or table allocates a new
+ * one and keeps the old one allocated, so replays stay valid; the kept buffers
+ * are freed when the context's last graph is destroyed, or at shutdown.
+ * Graphs may outlive the context (destroying one later is safe), but must not
+ * be launched after tmac_shutdown. */
 int tmac_step_end(tmac_context* ctx, tmac_stream stream, tmac_graph** graph);
 int tmac_graph_launch(tmac_context* ctx, tmac_graph* graph, tmac_stream stream);
 int tmac_graph_destroy(tmac_context* ctx, tmac_graph* graph);
@@ -383,6 +390,16 @@ int tmac_event_record(tmac_context* ctx, tmac_event ev, tmac_stream stream);
 int tmac_event_elapsed_ms(tmac_context* ctx, tmac_event start, tmac_event stop, float* ms);
 /* Device facts: compute units, HBM bus width etc. are in the returned text. */
 int tmac_device_info(tmac_context* ctx, char* buf, size_t buf_len, int* n_cu);
+
+/* ---- synthetic workload streams (host only; no counterpart in the reference, which reads model
+ *      weights and prompt tokens) ----
+ * Stream `seed`: splitmix64 expands the seed into the state of xoshiro256**.  tmac_synth_uniform
+ * writes n uniforms in [0, 1) (the top 53 bits of each output times 2^-53); tmac_synth_normal writes
+ * n N(0,1) values, two per Box-Muller pair in double precision (radius sqrt(-2 ln(1 - u1)), angle
+ * 2 pi u2; cos then sin), each rounded to fp32.  The benchmark and the parity tests draw their inputs
+ * from these streams, so both see the same values.  No context, no GPU. */
+int tmac_synth_normal(uint64_t seed, float* out, size_t n);
+int tmac_synth_uniform(uint64_t seed, double* out, size_t n);
 
 #ifdef __cplusplus
 }

@@ -26,6 +26,12 @@ LIB_DIR = os.path.join(HERE, "lib")
 PARITY_LIB = os.path.join(LIB_DIR, "libtmac_oracle.so")
 TIMING_LIB = os.path.join(LIB_DIR, "libtmac_oracle_o3.so")
 
+# Compiler flags of the two builds (oracle/Makefile; a CPU test keeps the two in step).
+BUILD_FLAGS = {
+    "parity": "gcc -std=c11 -O2 -ffp-contract=off -fno-fast-math -fno-builtin -fopenmp -fPIC",
+    "timing": "gcc -std=c11 -O3 -fopenmp -fPIC",
+}
+
 _F = ctypes.POINTER(ctypes.c_float)
 _I64 = ctypes.POINTER(ctypes.c_int64)
 _I32 = ctypes.POINTER(ctypes.c_int32)

@@ -287,3 +287,14 @@ def test_bad_arguments_are_rejected():
         oracle.attention(q, k, k, NH, 3, HD, 2)
     with pytest.raises(ValueError):
         oracle.attention(q, k, k, NH, NKV, HD, -1)
+
+
+def test_build_flags_match_makefile():
+    """oracle.BUILD_FLAGS (reported with the CPU baseline) are the flags oracle/Makefile compiles with."""
+    import os
+    import re
+    mk = open(os.path.join(os.path.dirname(oracle.__file__), "Makefile")).read()
+    lines = [" ".join(l.replace("\\\n", " ").split()) for l in re.findall(r"\$\(CC\)[^\n]*(?:\\\n[^\n]*)*", mk)]
+    for name, flags in oracle.BUILD_FLAGS.items():
+        words = flags.split()[1:]
+        assert any(all(w in ln.split() for w in words) for ln in lines), (name, flags, lines)

@@ -76,6 +76,7 @@ struct RopeTable {
 
 struct tmac_graph {
     hipGraphExec_t exec = nullptr;
+    tmac_context* owner = nullptr;  // counted in owner->live_graphs while exec is set
 };
 
 struct tmac_model {
@@ -121,6 +122,14 @@ struct tmac_context {
     size_t ws_floats = 0;
     int* err = nullptr;
     std::vector<RopeTable> rope;
+    // Executable step graphs alive on this context.  A captured graph keeps
+    // the workspace and RoPE-table addresses it was recorded with, so while
+    // any graph is alive a buffer replaced by a larger one is retired (kept
+    // allocated) instead of freed; retired buffers are freed when the last
+    // graph is destroyed, or at shutdown.
+    int live_graphs = 0;
+    std::vector<void*> retired;
+    std::vector<tmac_graph*> graphs;  // the live graphs, detached from the context at shutdown
     int64_t opt_split_len = 0;
     int64_t opt_target_groups = 0;
     int64_t opt_kernel = TMAC_KERNEL_AUTO;
@@ -292,6 +301,34 @@ bool use_head_kernel(const tmac_context* ctx, int n_seq, int n_head, int rows) {
     return (int64_t)n_seq * n_head < 2LL * ctx->n_cu && rows <= kHeadMaxRows;
 }
 
+// Frees a device buffer the context no longer uses, or retires it while a
+// step graph that may have recorded its address is alive.
+void release_buffer(tmac_context* ctx, void* p) {
+    if (!p) return;
+    if (ctx->live_graphs > 0)
+        ctx->retired.push_back(p);
+    else
+        (void)hipFree(p);
+}
+
+// Drops a graph from its context's live count (its executable is gone).
+void forget_graph(tmac_graph* g) {
+    tmac_context* ctx = g->owner;
+    g->owner = nullptr;
+    if (!ctx) return;
+    ctx->live_graphs--;
+    auto it = std::find(ctx->graphs.begin(), ctx->graphs.end(), g);
+    if (it != ctx->graphs.end()) ctx->graphs.erase(it);
+}
+
+void free_retired(tmac_context* ctx) {
+    if (ctx->retired.empty()) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();
+    for (void* p : ctx->retired) (void)hipFree(p);
+    ctx->retired.clear();
+}
+
 int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats) {
     if (floats <= ctx->ws_floats) return TMAC_OK;
     if (capturing(stream))
@@ -304,7 +341,7 @@ int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats) {
         while (n < floats) n *= 2;
         float* p = nullptr;
         HIP_TRY(ctx, hipMalloc(&p, n * sizeof(float)));
-        if (ctx->ws) (void)hipFree(ctx->ws);
+        release_buffer(ctx, ctx->ws);
         ctx->ws = p;
         ctx->ws_floats = n;
     }
@@ -354,7 +391,7 @@ int rope_table(tmac_context* ctx, hipStream_t stream, int head_dim, float base, 
     HIP_TRY(ctx, hipMalloc(&dev, host.size() * sizeof(float2)));
     HIP_TRY(ctx, hipMemcpy(dev, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice));
     if (found) {
-        (void)hipFree(found->dev);
+        release_buffer(ctx, found->dev);
         found->dev = dev;
         found->rows = new_rows;
     } else {
@@ -507,7 +544,7 @@ int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, unsig
     int rc = ensure_workspace(ctx, stream, slots * slot_floats + 2 * (size_t)n_seq);
     if (rc) return rc;
     a.ws = ctx->ws;
-    a.seg_meta = reinterpret_cast<int32_t*>(ctx->ws + slots * slot_floats);
+    a.seg_meta = reinterpret_cast<int32_t*>(a.ws + slots * slot_floats);
     a.split_len = 0;
     a.n_splits = (int)units;
     a.n_seq = n_seq;
@@ -707,6 +744,8 @@ int tmac_shutdown(tmac_context* ctx) {
         (void)hipDeviceSynchronize();
         for (auto& t : ctx->rope) (void)hipFree(t.dev);
         if (ctx->ws) (void)hipFree(ctx->ws);
+        for (void* p : ctx->retired) (void)hipFree(p);
+        for (tmac_graph* g : ctx->graphs) g->owner = nullptr;  // graphs destroyed later touch no context
         if (ctx->err) (void)hipFree(ctx->err);
         for (auto& m : ctx->modules)
             if (m) (void)hipModuleUnload(m);
@@ -1349,6 +1388,7 @@ int tmac_step_end(tmac_context* ctx, tmac_stream stream, tmac_graph** graph) {
         (void)hipGetLastError();
         (void)hipGraphExecDestroy((*graph)->exec);
         (*graph)->exec = nullptr;
+        forget_graph(*graph);
     }
     hipGraphExec_t exec = nullptr;
     hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
@@ -1356,6 +1396,9 @@ int tmac_step_end(tmac_context* ctx, tmac_stream stream, tmac_graph** graph) {
     if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
     if (!*graph) *graph = new tmac_graph();
     (*graph)->exec = exec;
+    (*graph)->owner = ctx;
+    ctx->live_graphs++;
+    ctx->graphs.push_back(*graph);
     return TMAC_OK;
 }
 
@@ -1371,7 +1414,10 @@ int tmac_graph_destroy(tmac_context* ctx, tmac_graph* graph) {
     (void)ctx;
     if (!graph) return TMAC_OK;
     if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    tmac_context* owner = graph->owner;
+    forget_graph(graph);
     delete graph;
+    if (owner && owner->live_graphs == 0) free_retired(owner);
     return TMAC_OK;
 }
 

@@ -104,6 +104,8 @@ SIGNATURES = {
     "tmac_set_option": (_i, [_vp, _i, _i64]),
     "tmac_query_split": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "tmac_check_device_error": (_i, [_vp]),
+    "tmac_synth_normal": (_i, [ctypes.c_uint64, _vp, _sz]),
+    "tmac_synth_uniform": (_i, [ctypes.c_uint64, _vp, _sz]),
     "tmac_step_begin": (_i, [_vp, _vp]),
     "tmac_step_end": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
     "tmac_graph_launch": (_i, [_vp, _vp, _vp]),
@@ -208,6 +210,26 @@ class TmacError(RuntimeError):
 
 def status_string(status: int) -> str:
     return load_library().tmac_status_string(status).decode()
+
+
+def synth_normal(seed: int, shape, out: Optional[np.ndarray] = None) -> np.ndarray:
+    """N(0,1) fp32 values of stream `seed` (tmac_synth_normal; host only, no GPU)."""
+    if out is None:
+        out = np.empty(shape, np.float32)
+    assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+    rc = load_library().tmac_synth_normal(ctypes.c_uint64(seed), out.ctypes.data, out.size)
+    if rc:
+        raise TmacError(rc, "synth_normal")
+    return out
+
+
+def synth_uniform(seed: int, n: int) -> np.ndarray:
+    """Uniforms in [0, 1) of stream `seed` (tmac_synth_uniform)."""
+    out = np.empty(n, np.float64)
+    rc = load_library().tmac_synth_uniform(ctypes.c_uint64(seed), out.ctypes.data, n)
+    if rc:
+        raise TmacError(rc, "synth_uniform")
+    return out
 
 
 class DeviceArray:
