@@ -190,6 +190,20 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
                                  const float* k_pool, const float* v_pool, const int64_t* offsets,
                                  const int32_t* lengths, float* out, int n_seq, int n_head,
                                  int n_kv_head, int head_dim, int max_len, int64_t total_rows);
+/* tmac_attention_decode_ragged with no allocation: no counterpart in the reference.  For callers
+ * that cannot allocate device memory (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, kernels and results; the split-KV partials go to a fixed
+ * device array of TMAC_SCRATCH_BYTES that the library holds on each GPU from tmac_init until the
+ * process ends, instead of the context's growable workspace, and the call never calls hipMalloc or
+ * hipFree.  A call whose schedule needs more than TMAC_SCRATCH_BYTES of partials launches nothing and
+ * returns TMAC_ERR_CAPACITY (at 14 query heads: stream-K batches up to about 4,000 sequences, unit-grid
+ * batches up to n_seq * splits = 4,500).  Every call on one GPU shares that GPU's array (all contexts
+ * and streams): calls that overlap on one GPU race.  No part of it needs to start at zero. */
+#define TMAC_SCRATCH_BYTES (16u << 20)
+int tmac_attention_decode_ragged_noalloc(tmac_context* ctx, tmac_stream stream, const float* q,
+                                         const float* k_pool, const float* v_pool, const int64_t* offsets,
+                                         const int32_t* lengths, float* out, int n_seq, int n_head,
+                                         int n_kv_head, int head_dim, int max_len, int64_t total_rows);
 
 /* ---- TMAC weight file: load_tmac (tmac_gguf.cpp:1372-1425) ----
  * The file scripts/extract_tmac.py writes (its :1-24, 261-272):

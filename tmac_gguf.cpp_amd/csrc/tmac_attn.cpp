@@ -31,6 +31,8 @@
 constexpr int kCodeParts = 4;
 extern "C" const unsigned char* const tmac_attn_code_objects[kCodeParts];
 extern "C" const uint64_t tmac_attn_code_object_sizes[kCodeParts];
+// tmac_scratch.hip: the device address of the fixed scratch array on `device` (the current device).
+extern "C" int tmac_scratch_setup(int device, void** ptr);
 
 using tmac::CopyArgs;
 using tmac::CvtArgs;
@@ -129,6 +131,14 @@ struct tmac_context {
     // graph is destroyed, or at shutdown.
     int live_graphs = 0;
     std::vector<void*> retired;
+    // Device address of the fixed scratch array on this context's device
+    // (TMAC_SCRATCH_BYTES), resolved once at init.
+    float* scratch = nullptr;
+    // Set only for the duration of a call of an entry point that allocates
+    // nothing: the workspace is then this fixed buffer of fixed_floats floats
+    // instead of ws, and nothing grows.
+    float* fixed_ws = nullptr;
+    size_t fixed_floats = 0;
     std::vector<tmac_graph*> graphs;  // the live graphs, detached from the context at shutdown
     int64_t opt_split_len = 0;
     int64_t opt_target_groups = 0;
@@ -301,6 +311,22 @@ bool use_head_kernel(const tmac_context* ctx, int n_seq, int n_head, int rows) {
     return (int64_t)n_seq * n_head < 2LL * ctx->n_cu && rows <= kHeadMaxRows;
 }
 
+// The split-KV workspace of the current call (valid after ensure_workspace).
+float* workspace(const tmac_context* ctx) { return ctx->fixed_ws ? ctx->fixed_ws : ctx->ws; }
+
+// Makes the fixed scratch buffer the workspace for one call.
+struct FixedWorkspace {
+    tmac_context* ctx;
+    FixedWorkspace(tmac_context* c, float* p, size_t floats) : ctx(c) {
+        ctx->fixed_ws = p;
+        ctx->fixed_floats = floats;
+    }
+    ~FixedWorkspace() {
+        ctx->fixed_ws = nullptr;
+        ctx->fixed_floats = 0;
+    }
+};
+
 // Frees a device buffer the context no longer uses, or retires it while a
 // step graph that may have recorded its address is alive.
 void release_buffer(tmac_context* ctx, void* p) {
@@ -330,6 +356,13 @@ void free_retired(tmac_context* ctx) {
 }
 
 int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats) {
+    if (ctx->fixed_ws) {
+        if (floats <= ctx->fixed_floats) return TMAC_OK;
+        return fail(ctx, TMAC_ERR_CAPACITY,
+                    "the call needs " + std::to_string(floats * sizeof(float)) +
+                        " bytes of split-KV workspace, more than the fixed scratch buffer's " +
+                        std::to_string(ctx->fixed_floats * sizeof(float)) + " (TMAC_SCRATCH_BYTES)");
+    }
     if (floats <= ctx->ws_floats) return TMAC_OK;
     if (capturing(stream))
         return fail(ctx, TMAC_ERR_CAPTURE,
@@ -441,7 +474,7 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
         const size_t need = (size_t)n_seq * n_splits * a.n_head * kPartialStride;
         int rc = ensure_workspace(ctx, stream, need);
         if (rc) return rc;
-        a.ws = ctx->ws;
+        a.ws = workspace(ctx);
     } else {
         a.ws = nullptr;
     }
@@ -543,7 +576,7 @@ int run_decode_sk(tmac_context* ctx, hipStream_t stream, hipFunction_t sk, unsig
     const size_t slots = (size_t)units + (size_t)n_seq;
     int rc = ensure_workspace(ctx, stream, slots * slot_floats + 2 * (size_t)n_seq);
     if (rc) return rc;
-    a.ws = ctx->ws;
+    a.ws = workspace(ctx);
     a.seg_meta = reinterpret_cast<int32_t*>(a.ws + slots * slot_floats);
     a.split_len = 0;
     a.n_splits = (int)units;
@@ -733,6 +766,10 @@ int tmac_init(tmac_context** out, int device) {
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
     int rc = ensure_workspace(ctx, nullptr, (size_t)1 << 20);
     if (rc) return bail(rc);
+    void* scratch = nullptr;
+    if ((e = (hipError_t)tmac_scratch_setup(device, &scratch)) != hipSuccess)
+        return bail(hip_fail(ctx, e, "hipGetSymbolAddress(scratch)"));
+    ctx->scratch = static_cast<float*>(scratch);
     *out = ctx;
     return TMAC_OK;
 }
@@ -852,6 +889,18 @@ int tmac_attention_decode_ragged(tmac_context* ctx, tmac_stream stream, const fl
                                  const float* k_pool, const float* v_pool, const int64_t* offsets,
                                  const int32_t* lengths, float* out, int n_seq, int n_head,
                                  int n_kv_head, int head_dim, int max_len, int64_t total_rows) {
+    return decode_ragged_impl(ctx, stream, TMAC_KV_F32, q, k_pool, v_pool, offsets, lengths, out, n_seq, n_head,
+                              n_kv_head, head_dim, max_len, total_rows);
+}
+
+int tmac_attention_decode_ragged_noalloc(tmac_context* ctx, tmac_stream stream, const float* q,
+                                         const float* k_pool, const float* v_pool, const int64_t* offsets,
+                                         const int32_t* lengths, float* out, int n_seq, int n_head,
+                                         int n_kv_head, int head_dim, int max_len, int64_t total_rows) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!ctx->scratch) return fail(ctx, TMAC_ERR_NOT_INITIALIZED, "decode_ragged_noalloc: no scratch buffer");
+    FixedWorkspace fixed(ctx, ctx->scratch, TMAC_SCRATCH_BYTES / sizeof(float));
     return decode_ragged_impl(ctx, stream, TMAC_KV_F32, q, k_pool, v_pool, offsets, lengths, out, n_seq, n_head,
                               n_kv_head, head_dim, max_len, total_rows);
 }
@@ -1091,7 +1140,7 @@ static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const flo
     const size_t pack_bytes = (size_t)pack_blocks * kPrefillTileElems * sizeof(uint16_t);
     if ((rc = ensure_workspace(ctx, (hipStream_t)stream, pack_bytes / sizeof(float)))) return rc;
     PrefillArgs a{q, static_cast<const float*>(k_cache), static_cast<const float*>(v_cache), out, seq_stride, n_q,
-                  prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(ctx->ws), n_tp, n_rows,
+                  prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(workspace(ctx)), n_tp, n_rows,
                   block_table, max_pages, n_pages, ctx->err};
     if ((rc = launch(ctx, ctx->prefill_pack[block_table ? 1 : 0][dt].at(n_kv_head), (unsigned)pack_blocks, 1, 256,
                      (hipStream_t)stream, &a)))

@@ -97,6 +97,8 @@ SIGNATURES = {
     "tmac_rope_prepare": (_i, [_vp, _i, _f, _i]),
     "tmac_attention_decode_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
     "tmac_attention_decode_ragged": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64]),
+    "tmac_attention_decode_ragged_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                                  _i64]),
     "tmac_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_attention_prefill_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_attention_prefill_paged": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i]),
