@@ -197,11 +197,25 @@ def bench_c1(ctx, stream, steps=200, warmup=20):
         ctx.attention_op(dq, dk, dv, dout, NH, NKV, HD, 255, stream=stream)
 
     per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
+    # 100 calls recorded into one graph (the reference encodes its dispatches into
+    # one command buffer): GPU time per call with no host launch cost in it
+    n_calls = 100
+    ctx.step_begin(stream)
+    for _ in range(n_calls):
+        launch()
+    g = ctx.step_end(stream)
+    per_g, mean_g = time_launches(ctx, stream, lambda: ctx.graph_launch(g, stream), 20, 5)
+    ctx.graph_destroy(g)
     for d in (dq, dk, dv, dout):
         d.free()
-    return {"median_us": float(np.median(per)) * 1e3, "p10_us": pct(per, 10) * 1e3,
+    return {"graph_us_per_call": mean_g * 1e3 / n_calls,
+            "eager_mean_us": mean_ms * 1e3,
+            "median_us": float(np.median(per)) * 1e3, "p10_us": pct(per, 10) * 1e3,
             "p90_us": pct(per, 90) * 1e3, "mean_us": mean_ms * 1e3,
-            "bytes": algo_bytes([256])}
+            "bytes": algo_bytes([256]),
+            "note": "graph_us_per_call: 100 attention_op calls captured in one graph, GPU time per call; "
+                    "eager_mean_us: back-to-back eager calls from Python (host launch rate bound); "
+                    "median/p10/p90: one eager call between two events"}
 
 
 def bench_c2(ctx, stream, layers=24, cap=256, use_graph=True):
@@ -273,6 +287,8 @@ def c2_graph(ctx, stream, layer, pos, layers, cap):
     ctx.graph_destroy(g)
     step_bytes = [layers * (1024 * s + 9216) for s in range(1, cap + 1)]
     return {"median_step_us": float(np.median(per)), "p90_step_us": pct(per, 90),
+            "p10_step_us": pct(per, 10), "max_step_us": float(per.max()),
+            "step_us_s1": float(per[0]), "step_us_s128": float(per[127]),
             "step_us_s256": float(per[-1]),
             "gbs_s256": step_bytes[-1] / (per[-1] * 1e-6) / 1e9,
             "nodes_per_step": layers + 1}
@@ -569,7 +585,8 @@ def main():
     sections = set(x for x in args.sections.split(",") if x) if not args.only_c3 else set()
     if "c1" in sections:
         extra["c1"] = bench_c1(ctx, stream)
-        log(f"[bench] C1 {extra['c1']['median_us']:.2f} us/call")
+        log(f"[bench] C1 {extra['c1']['graph_us_per_call']:.2f} us/call in a graph, "
+            f"{extra['c1']['eager_mean_us']:.2f} us/call eager, {extra['c1']['median_us']:.2f} us per evented call")
     if "c2" in sections or "c2eager" in sections:
         extra["c2"] = bench_c2(ctx, stream, use_graph="c2" in sections)
         log(f"[bench] C2 {extra['c2']}")

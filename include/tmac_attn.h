@@ -344,18 +344,23 @@ enum tmac_option {
     TMAC_OPT_GROUP_WAVES = 7,   /* fp32 group kernel workgroup size in waves: 4 or 8; 0 (default) = 4 unless a
                                    split would hold fewer than 64 rows, then 8 */
     TMAC_OPT_MFMA_DECODE = 8,   /* 1 (default): bf16/fp16/Q8_0 caches use the MFMA group kernel (decode and layer step) where one exists; 0: VALU */
-    TMAC_OPT_STREAM_K = 9       /* ragged and paged decode schedule: 1 (default) = automatic, 2 = always stream-K
+    TMAC_OPT_STREAM_K = 9,      /* ragged and paged decode schedule: 1 (default) = automatic, 2 = always stream-K
                                    (the batch's rows cut into equal ranges, one workgroup each), 0 = never (one
                                    workgroup per (sequence, split) unit).  Stream-K is not used when
                                    TMAC_OPT_SPLIT_LEN is set, the head kernel is chosen or (narrow caches) the MFMA
                                    decode is off; automatic picks it, in sequences per CU, for 0.5 to 1.5 or more
                                    than 10 (fp32 ragged), from 0.5 (fp32 paged), up to 2 or more than 10 (fp32
                                    paged layer step), above 10 (bf16 / fp16 / Q8_0) */
+    TMAC_OPT_HV_SPLIT = 10      /* split-V head kernel: workgroups per query head (1, 2, 4 or 8; default 8), each
+                                   scoring every row and accumulating 64/value dims of V */
 };
 enum tmac_kernel_choice {
-    TMAC_KERNEL_AUTO = 0,   /* head kernel for short contexts on few sequences, else group */
+    TMAC_KERNEL_AUTO = 0,   /* short contexts on few sequences: the split-V head kernel (fp32 caches) or
+                               the head kernel (bf16 / fp16 / Q8_0); else group */
     TMAC_KERNEL_GROUP = 1,  /* workgroup per (split, sequence), each K/V byte read once */
-    TMAC_KERNEL_HEAD = 2    /* workgroup per (query head, sequence), no split merge */
+    TMAC_KERNEL_HEAD = 2,   /* workgroup per (query head, sequence), no split merge; 8 lanes per row */
+    TMAC_KERNEL_HEADV = 3   /* the same, each query head's V dims split over TMAC_OPT_HV_SPLIT
+                               workgroups (fp32 caches; other caches use the head kernel) */
 };
 int tmac_set_option(tmac_context* ctx, int option, int64_t value);
 /* Rows per workgroup and splits the next decode with this shape would use

@@ -17,7 +17,7 @@ from conftest import assert_close
 pytestmark = pytest.mark.gpu
 
 KERNELS = {"auto": tmac_attn.TMAC_KERNEL_AUTO, "group": tmac_attn.TMAC_KERNEL_GROUP,
-           "head": tmac_attn.TMAC_KERNEL_HEAD}
+           "head": tmac_attn.TMAC_KERNEL_HEAD, "headv": tmac_attn.TMAC_KERNEL_HEADV}
 
 
 @pytest.fixture(params=list(KERNELS))
@@ -266,4 +266,53 @@ def test_graph_24_layer_step_replay(ctx):
     finally:
         ctx.graph_destroy(g)
         ctx.destroy_stream(s)
+    assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("split", [1, 2, 4, 8])
+def test_split_v_head_kernel(ctx, split):
+    """The split-V head kernel with each V split: attention_op, a short ragged batch with an
+    empty and an over-long sequence, and the layer step at several positions (cache rows
+    bit-exact)."""
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_HEADV)
+    ctx.set_option(tmac_attn.TMAC_OPT_HV_SPLIT, split)
+    try:
+        for past_len in (0, 9, 255, 700):
+            k, v = rand_cache(1300 + past_len, past_len + 1)
+            q = oracle.normal(1301 + past_len, NH * HD)
+            dq, dk, dv, dout = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.empty(NH * HD)
+            ctx.attention_op(dq, dk, dv, dout, NH, NKV, HD, past_len)
+            assert_close(dout.numpy(), oracle.attention(q, k, v, NH, NKV, HD, past_len),
+                         f"attention_op split {split} past_len {past_len}")
+        lens = np.array([3, 0, 64, 129, 500], np.int32)
+        offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
+        k, v = rand_cache(1310, int(lens.sum()))
+        q = oracle.normal(1311, (lens.size, NH * HD))
+        nz = lens > 0
+        ref = np.zeros((lens.size, NH * HD), np.float32)
+        ref[nz] = oracle.attention_ragged(q[nz], k, v, offs[nz], lens[nz], NH, NKV, HD, n_threads=8)
+        dq, dk, dv, do, dl = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.upload(offs), ctx.upload(lens)
+        dout = ctx.empty((lens.size, NH * HD))
+        ctx.decode_ragged(dq, dk, dv, do, dl, dout, lens.size, NH, NKV, HD, 500)
+        assert_close(dout.numpy(), ref, f"ragged split {split}")
+        ctx.decode_ragged(dq, dk, dv, do, dl, dout, lens.size, NH, NKV, HD, 200)  # 500 > max_len: NaN, bit 1
+        got = dout.numpy()
+        assert np.all(np.isnan(got[4])) and np.all(got[1] == 0)
+        assert ctx.check_device_error() == tmac_attn.TMAC_ERR_DEVICE_FAULT
+        for pos in (0, 1, 100, 255):
+            cap = 256
+            kc, vc = np.zeros((cap, KVD), np.float32), np.zeros((cap, KVD), np.float32)
+            if pos:
+                kc[:pos], vc[:pos] = rand_cache(1320 + pos, pos)
+            q, kn, vn = oracle.normal(1330 + pos, NH * HD), oracle.normal(1331 + pos, KVD), oracle.normal(1332 + pos, KVD)
+            dq, dkn, dvn, dkc, dvc = ctx.upload(q), ctx.upload(kn), ctx.upload(vn), ctx.upload(kc), ctx.upload(vc)
+            dout = ctx.empty(NH * HD)
+            ctx.layer_attention(dq, dkn, dvn, dkc, dvc, dout, NH, NKV, HD, pos, cap, 1e6)
+            ref, _, _ = oracle.layer_step(q, kn, vn, kc, vc, NH, NKV, HD, pos, 1e6)
+            assert_close(dout.numpy(), ref, f"layer split {split} pos {pos}")
+            np.testing.assert_array_equal(dkc.numpy(), kc)
+            np.testing.assert_array_equal(dvc.numpy(), vc)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_AUTO)
+        ctx.set_option(tmac_attn.TMAC_OPT_HV_SPLIT, 8)
     assert ctx.check_device_error() == 0

@@ -19,6 +19,9 @@ constexpr int kPageShift = 4;       // log2(kPageRows)
 constexpr int kMWavesHost = 8;      // MFMA decode kernel: waves per workgroup
 constexpr int kHeadWaves = 16;      // "head" decode kernel (short contexts): 1024 threads
 constexpr int kHeadPrefetchDepth = 2;
+constexpr int kHvWaves = 8;         // split-V head kernel (short contexts): 512 threads
+constexpr int kHvDepth = 2;         // split-V head kernel: steps of K/V in flight per wave
+constexpr int kHvSplitDefault = 8;  // workgroups per query head, each accumulating 64/8 dims of V
 constexpr int kMaxSplits = 256;     // split-KV workgroups per sequence, at most
 constexpr int kPartialStride = kHeadDim + 2;  // per (split, head): acc[64], m, l
 

@@ -1157,6 +1157,262 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     finish<1, 1, NW>(st, lane, wave, true, out_head, nullptr);
 }
 
+// Sum over all 64 lanes of a wave; every lane receives the same bits (each
+// step adds a value and its partner's, which commute exactly).
+__device__ __forceinline__ float wave_sum(float x) {
+    x = slot_sum(x);     // 8 lanes
+    x += dpp<0x140>(x);  // row_mirror: lane i <- lane 15 - i
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Short-context decode with V split over workgroups ("split-V head"
+// kernel; fp32 caches).  grid = (query head x VS, sequence), one split.
+// Short contexts leave all but a few CUs idle, and each workgroup of the head
+// kernel moves its kv head's full K and V half rows (128 KB at 256 rows)
+// through one CU, at roughly 80 GB/s per CU.  Here VS workgroups serve one
+// query head: each scores all rows (full K) but accumulates only 64/VS dims
+// of V, so a CU moves 256 + 256/VS bytes per row instead of 512; the scores
+// are computed VS times, from L2.
+//   * Lane layout as the head kernel: 8 lanes per row, lane c holds K dims
+//     {4c..4c+3, 32+4c..32+4c+3} and DV = 8/VS V dims (vdim0 .. vdim0+DV-1).
+//   * Layer mode: the new cache row is rotated and stored right after the
+//     position is known, before the rows are attended, so its store latency
+//     overlaps the attention; workgroup (head, p) of the group's first head
+//     stores V dims of part p, part 0 also the K row.
+template <int VS>
+__device__ __forceinline__ int hv_vdim0(int vp, int c) {
+    return VS == 1 ? 4 * c : VS == 2 ? 32 * vp + 4 * c : VS == 4 ? 16 * vp + 2 * c : 8 * vp + c;
+}
+
+template <int DV>
+struct VPart {
+    float x[DV];
+};
+
+template <int VS>
+__device__ __forceinline__ void hv_load(VPart<8 / VS>& v, const float* __restrict__ p) {
+    if constexpr (VS == 1) {
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        const float4 b = *reinterpret_cast<const float4*>(p + 32);
+        v.x[0] = a.x; v.x[1] = a.y; v.x[2] = a.z; v.x[3] = a.w;
+        v.x[4] = b.x; v.x[5] = b.y; v.x[6] = b.z; v.x[7] = b.w;
+    } else if constexpr (VS == 2) {
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        v.x[0] = a.x; v.x[1] = a.y; v.x[2] = a.z; v.x[3] = a.w;
+    } else if constexpr (VS == 4) {
+        const float2 a = *reinterpret_cast<const float2*>(p);
+        v.x[0] = a.x; v.x[1] = a.y;
+    } else {
+        v.x[0] = *p;
+    }
+}
+
+template <int VS>
+__device__ __forceinline__ void hv_store(float* __restrict__ p, const VPart<8 / VS>& v) {
+    if constexpr (VS == 1) {
+        *reinterpret_cast<float4*>(p) = make_float4(v.x[0], v.x[1], v.x[2], v.x[3]);
+        *reinterpret_cast<float4*>(p + 32) = make_float4(v.x[4], v.x[5], v.x[6], v.x[7]);
+    } else if constexpr (VS == 2) {
+        *reinterpret_cast<float4*>(p) = make_float4(v.x[0], v.x[1], v.x[2], v.x[3]);
+    } else if constexpr (VS == 4) {
+        *reinterpret_cast<float2*>(p) = make_float2(v.x[0], v.x[1]);
+    } else {
+        *p = v.x[0];
+    }
+}
+
+// V dim t of this lane's part -> position in the head's 64 output dims.
+template <int VS>
+__device__ __forceinline__ int hv_dim(int vdim0, int t) {
+    return VS == 1 ? vdim0 + (t < 4 ? t : 28 + t) : vdim0 + t;
+}
+
+template <int G, int KV, int NW, int DEPTH, int MODE, int VS>
+__device__ __forceinline__ void hv_body(const DecodeArgs& a) {
+    static_assert(MODE == kUniform || MODE == kRagged || MODE == kLayer, "split-V head kernel modes");
+    constexpr int DV = 8 / VS;
+    constexpr int ROWF = KV * kHeadDim;  // floats per cache row
+    constexpr int NH = KV * G;
+    constexpr int PPS = kSlots;          // rows per step (one kv head)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int head = blockIdx.x / VS, vp = blockIdx.x % VS, seq = blockIdx.y;
+    const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
+    const int kvh = head / G;
+    const int vdim0 = hv_vdim0<VS>(vp, c);
+
+    // 1. loads that do not depend on the length
+    float q[1][kDimsPerLane];
+    load8(q[0], a.q + ((size_t)seq * NH + head) * kHeadDim + 4 * c);
+    float kn[kDimsPerLane];
+    VPart<DV> vn;
+    const bool new_lane = (MODE == kLayer) && wave == 0 && slot == 0;
+    if (new_lane) {
+        load8(kn, a.k_new + kvh * kHeadDim + 4 * c);
+        hv_load<VS>(vn, a.v_new + kvh * kHeadDim + vdim0);
+    }
+    size_t base = 0;
+    int bound;
+    if (MODE == kUniform) {
+        base = (size_t)seq * (size_t)a.seq_stride;
+        bound = a.n_pos;
+    } else if (MODE == kRagged) {
+        base = (size_t)a.offsets[seq];
+        bound = a.lengths[seq];
+    } else {
+        bound = a.capacity;
+    }
+    const float* kb = a.k + base * ROWF + (size_t)(wave * PPS + slot) * ROWF + kvh * kHeadDim + 4 * c;
+    const float* vb = a.v + base * ROWF + (size_t)(wave * PPS + slot) * ROWF + kvh * kHeadDim + vdim0;
+    // float offset (from kb / vb) of this lane's row in the wave's k-th step, rows clamped below lim
+    auto row_off = [&](int k, int lim) {
+        const int row = (wave + NW * k) * PPS + slot;
+        const int r = min(row, lim - 1);
+        return (ptrdiff_t)(r - wave * PPS - slot) * ROWF;
+    };
+    float kbuf[DEPTH][kDimsPerLane];
+    VPart<DV> vbuf[DEPTH];
+    if (MODE != kRagged || bound > 0) {  // step 0 speculatively (rows < bound are allocated)
+        load8(kbuf[0], kb + row_off(0, bound));
+        hv_load<VS>(vbuf[0], vb + row_off(0, bound));
+    }
+
+    // 2. the attended length
+    int n_pos, pos = 0;
+    if (MODE == kLayer) {
+        pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+        if (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) {
+            if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
+            return;
+        }
+        n_pos = pos + 1;
+    } else {
+        n_pos = bound;
+    }
+    float* out_head = a.out + ((size_t)seq * NH + head) * kHeadDim;
+    if (n_pos <= 0) {  // ragged sequence with no rows: defined as a zero output
+        if (threadIdx.x < 8)
+            for (int t = 0; t < DV; ++t) out_head[hv_dim<VS>(hv_vdim0<VS>(vp, threadIdx.x), t)] = 0.f;
+        return;
+    }
+    if (MODE == kRagged && n_pos > a.split_len) {  // longer than the max_len the launch was sized for
+        if (threadIdx.x < 8)
+            for (int t = 0; t < DV; ++t)
+                out_head[hv_dim<VS>(hv_vdim0<VS>(vp, threadIdx.x), t)] = __builtin_nanf("");
+        if (threadIdx.x == 0) atomicOr(a.err, 2);
+        return;
+    }
+    const int mem_rows = (MODE == kLayer) ? pos : n_pos;
+    const int n_steps = (mem_rows + PPS - 1) / PPS;
+    const int nk = (n_steps - wave + NW - 1) / NW;
+    const int lim = max(mem_rows, 1);
+#pragma unroll
+    for (int d = 1; d < DEPTH; ++d) {
+        load8(kbuf[d], kb + row_off(d, lim));
+        hv_load<VS>(vbuf[d], vb + row_off(d, lim));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 3. RoPE (layer mode): q, and the new row, stored now (tmac_gguf.cpp:1090-1091)
+    const float2* cs_row = nullptr;
+    if (MODE == kLayer) {
+        cs_row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
+        rope8(q[0], cs_row, c);
+        if (new_lane) {
+            rope8(kn, cs_row, c);
+            if (head % G == 0) {
+                if (vp == 0) store8(a.k_out + (size_t)pos * ROWF + kvh * kHeadDim + 4 * c, kn);
+                hv_store<VS>(a.v_out + (size_t)pos * ROWF + kvh * kHeadDim + vdim0, vn);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kDimsPerLane; ++t) q[0][t] *= a.qscale;
+
+    // 4. this wave's steps: wave + NW*k while the step starts below mem_rows
+    float m = kNegInf, l = 0.f, acc[DV];
+#pragma unroll
+    for (int t = 0; t < DV; ++t) acc[t] = 0.f;
+    auto attend_one = [&](const float (&kf)[kDimsPerLane], const VPart<DV>& vf, bool valid) {
+        float sc = q[0][0] * kf[0];
+#pragma unroll
+        for (int t = 1; t < kDimsPerLane; ++t) sc = fmaf(q[0][t], kf[t], sc);
+        sc = slot_sum(sc);
+        sc = valid ? sc : kNegInf;
+        if (__any(sc - m > kTau)) {  // raise the wave's shared max (rare after the first step)
+            float mx = sc;
+#pragma unroll
+            for (int mask = kLanesPerSlot; mask < 64; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
+            const float mn = fmaxf(m, mx);
+            const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
+            l *= alpha;
+#pragma unroll
+            for (int t = 0; t < DV; ++t) acc[t] *= alpha;
+            m = mn;
+        }
+        const float e = fast_exp2(sc - m);  // 0 for masked rows
+        l += e;
+#pragma unroll
+        for (int t = 0; t < DV; ++t) acc[t] = fmaf(e, valid ? vf.x[t] : 0.f, acc[t]);
+    };
+    for (int k0 = 0; k0 < nk; k0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int k = k0 + d;
+            if (k < nk) attend_one(kbuf[d], vbuf[d], (wave + NW * k) * PPS + slot < mem_rows);
+            load8(kbuf[d], kb + row_off(k + DEPTH, lim));
+            hv_load<VS>(vbuf[d], vb + row_off(k + DEPTH, lim));
+        }
+    }
+    // 5. layer mode: the new token (row pos) from registers, by wave 0
+    if (MODE == kLayer && wave == 0) {
+        if (!new_lane) {
+#pragma unroll
+            for (int t = 0; t < kDimsPerLane; ++t) kn[t] = 0.f;
+#pragma unroll
+            for (int t = 0; t < DV; ++t) vn.x[t] = 0.f;
+        }
+        attend_one(kn, vn, new_lane);
+    }
+
+    // 6. slots -> wave total (same max), then waves through LDS
+#pragma unroll
+    for (int mask = kLanesPerSlot; mask < 64; mask <<= 1) {
+        l += __shfl_xor(l, mask);
+#pragma unroll
+        for (int t = 0; t < DV; ++t) acc[t] += __shfl_xor(acc[t], mask);
+    }
+    __shared__ float s_acc[NW][kLanesPerSlot][DV];
+    __shared__ float s_ml[NW][2];
+    if (slot == 0) {
+#pragma unroll
+        for (int t = 0; t < DV; ++t) s_acc[wave][c][t] = acc[t];
+        if (c == 0) {
+            s_ml[wave][0] = m;
+            s_ml[wave][1] = l;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < kLanesPerSlot * DV) {
+        const int cc = threadIdx.x / DV, t = threadIdx.x % DV;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, s_ml[w][0]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = s_ml[w][0];
+            const float sc = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
+            L = fmaf(s_ml[w][1], sc, L);
+            A = fmaf(s_acc[w][cc][t], sc, A);
+        }
+        out_head[hv_dim<VS>(hv_vdim0<VS>(vp, cc), t)] = A / L;
+    }
+}
+
 // Log-sum-exp merge of the split partials: one wave per (head, sequence) with
 // more than one active split, lane d owning output dim d.  Splits go in
 // chunks of 32 whose loads are all issued before any is used: lane j loads
@@ -1253,6 +1509,13 @@ __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
 
 }  // namespace
 
+// Split-V head kernel, V split VS ways (grid x = n_head * VS).
+#define TMAC_HV_KERNEL(G, KV, M, MODE, VS)                                                         \
+    extern "C" __global__ __launch_bounds__(kHvWaves * 64) void tmac_##M##_hv##VS##_g##G##_kv##KV( \
+        DecodeArgs a) {                                                                            \
+        hv_body<G, KV, kHvWaves, kHvDepth, MODE, VS>(a);                                  \
+    }
+
 #define TMAC_MODE_KERNELS(G, KV, M, MODE)                                                          \
     extern "C" __global__ __launch_bounds__(kGroupWaves * 64) void tmac_##M##_g##G##_kv##KV(        \
         DecodeArgs a) {                                                                            \
@@ -1273,7 +1536,11 @@ __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(64) void tmac_##M##_combine_g##G##_kv##KV(DecodeArgs a) { \
         combine_body<G, KV, MODE>(a);                                                              \
-    }
+    }                                                                                              \
+    TMAC_HV_KERNEL(G, KV, M, MODE, 1)                                                              \
+    TMAC_HV_KERNEL(G, KV, M, MODE, 2)                                                              \
+    TMAC_HV_KERNEL(G, KV, M, MODE, 4)                                                              \
+    TMAC_HV_KERNEL(G, KV, M, MODE, 8)
 
 // Stream-K ragged decode (fp32 caches) and its combine.
 #define TMAC_SK_KERNELS(G, KV)                                                                     \
@@ -2494,12 +2761,7 @@ TMAC_MDECODE_KERNELS(8, 1)
 // (i < 16).  Every block field sits at an even offset, so the weights are read
 // as 16-bit words.  The dequantised weight d * q is exact in fp32; the row sum
 // is one fused multiply-add per element, then a wave reduction, so it differs
-// from the reference's sequential sum only by rounding.
-__device__ __forceinline__ float wave_sum(float x) {
-    x = slot_sum(x);
-    x += dpp<0x140>(x);  // row_mirror: lane i <- lane 15 - i, the other 8-lane half
-    return sum4_rows(x);
-}
+// from the reference's sequential sum only by rounding (wave_sum).
 
 __device__ __forceinline__ unsigned ld16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 

@@ -105,6 +105,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> head[3];     // head kernel (16 waves), same keys
     std::map<std::pair<int, int>, hipFunction_t> head8[3];    // head kernel, 8 waves
     std::map<std::pair<int, int>, hipFunction_t> head4[3];    // head kernel, 4 waves
+    std::map<std::pair<int, int>, hipFunction_t> hv[4][3];    // split-V head kernel by log2(V split), same keys
     std::map<std::pair<int, int>, hipFunction_t> combine[3];  // split merge, same keys
     std::map<std::pair<int, int>, hipFunction_t> decode_n[kNarrowTypes][3];  // bf16 / fp16 / Q8_0 caches: group kernel
     std::map<std::pair<int, int>, hipFunction_t> head_n[kNarrowTypes][3];    // the same: head kernel, 8 waves
@@ -149,6 +150,7 @@ struct tmac_context {
     int64_t opt_group_waves = 0;  // 0: automatic (auto_group_waves)
     int64_t opt_mfma = 1;
     int64_t opt_stream_k = 1;
+    int64_t opt_hv_split = tmac::kHvSplitDefault;
     std::string last_error;
     char device_name[256] = {0};
 };
@@ -199,6 +201,8 @@ bool capturing(hipStream_t s) {
 
 struct Kernels {
     hipFunction_t group = nullptr, head = nullptr, combine = nullptr;
+    hipFunction_t hv = nullptr;      // short-context split-V head kernel (fp32 caches, not paged)
+    int hv_split = 1;
     hipFunction_t group4 = nullptr;  // 4-wave group kernel when the size is chosen per call (fp32 caches)
     int head_waves = 16;
     int group_waves = 8;
@@ -230,7 +234,10 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
         k->head_waves = (int)ctx->opt_head_waves;
         k->head = (k->head_waves == 8 ? ctx->head8 : k->head_waves == 4 ? ctx->head4 : ctx->head)[mode].at({g, n_kv_head});
         k->combine = ctx->combine[mode].at({g, n_kv_head});
+        k->hv_split = (int)ctx->opt_hv_split;
+        k->hv = ctx->hv[__builtin_ctz(k->hv_split)][mode].at({g, n_kv_head});
         if (dt != TMAC_KV_F32) {
+            k->hv = nullptr;
             k->group4 = nullptr;
             k->group_waves = 8;
             k->group = ctx->decode_n[dt - 1][mode].at({g, n_kv_head});
@@ -238,6 +245,7 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
             k->head = ctx->head_n[dt - 1][mode].at({g, n_kv_head});
         }
         if (paged >= 0) {
+            k->hv = nullptr;
             k->group4 = nullptr;
             k->group_waves = kGroupWaves;
             k->group = ctx->paged[dt][paged].at({g, n_kv_head});
@@ -304,9 +312,10 @@ int auto_group_waves(const tmac_context* ctx, int n_seq, int rows, int n_kv_head
     return len >= kAuto4MinRows ? 4 : 8;
 }
 
-// Head kernel for short contexts that would leave most CUs idle otherwise.
+// One workgroup per query head (the row kernel, or the head kernel) for short
+// contexts that would leave most CUs idle otherwise.
 bool use_head_kernel(const tmac_context* ctx, int n_seq, int n_head, int rows) {
-    if (ctx->opt_kernel == TMAC_KERNEL_HEAD) return true;
+    if (ctx->opt_kernel == TMAC_KERNEL_HEAD || ctx->opt_kernel == TMAC_KERNEL_HEADV) return true;
     if (ctx->opt_kernel == TMAC_KERNEL_GROUP) return false;
     return (int64_t)n_seq * n_head < 2LL * ctx->n_cu && rows <= kHeadMaxRows;
 }
@@ -458,6 +467,9 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
         a.split_len = grid_rows;
         a.n_splits = 1;
         a.ws = nullptr;
+        if (k.hv && ctx->opt_kernel != TMAC_KERNEL_HEAD)
+            return launch(ctx, k.hv, (unsigned)(a.n_head * k.hv_split), (unsigned)n_seq, tmac::kHvWaves * 64, stream,
+                          &a);
         return launch(ctx, k.head, (unsigned)a.n_head, (unsigned)n_seq, k.head_waves * 64, stream, &a);
     }
     hipFunction_t group = k.group;
@@ -722,6 +734,12 @@ int tmac_init(tmac_context** out, int device) {
             if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
             ctx->head4[m][{sh[0], sh[1]}] = f;
+            for (int vs = 0; vs < 4; ++vs) {
+                std::snprintf(name, sizeof(name), "%s_hv%d_g%d_kv%d", mode_prefix[m], 1 << vs, sh[0], sh[1]);
+                if ((e = get_function(ctx, &f, name)) != hipSuccess)
+                    return bail(hip_fail(ctx, e, name));
+                ctx->hv[vs][m][{sh[0], sh[1]}] = f;
+            }
             std::snprintf(name, sizeof(name), "%s_combine_g%d_kv%d", mode_prefix[m], sh[0], sh[1]);
             if ((e = get_function(ctx, &f, name)) != hipSuccess)
                 return bail(hip_fail(ctx, e, name));
@@ -1363,8 +1381,14 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value) {
             ctx->opt_head_waves = value;
             return TMAC_OK;
         case TMAC_OPT_KERNEL:
-            if (value > TMAC_KERNEL_HEAD) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: bad kernel choice");
+            if (value < 0 || value > TMAC_KERNEL_HEADV)
+                return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: bad kernel choice");
             ctx->opt_kernel = value;
+            return TMAC_OK;
+        case TMAC_OPT_HV_SPLIT:
+            if (value != 1 && value != 2 && value != 4 && value != 8)
+                return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: V split must be 1, 2, 4 or 8");
+            ctx->opt_hv_split = value;
             return TMAC_OK;
         case TMAC_OPT_MFMA_DECODE:
             if (value > 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "set_option: MFMA decode is 0 or 1");

@@ -53,9 +53,11 @@ TMAC_OPT_WAVE_ORDER = 6
 TMAC_OPT_GROUP_WAVES = 7
 TMAC_OPT_MFMA_DECODE = 8
 TMAC_OPT_STREAM_K = 9
+TMAC_OPT_HV_SPLIT = 10
 TMAC_KERNEL_AUTO = 0
 TMAC_KERNEL_GROUP = 1
 TMAC_KERNEL_HEAD = 2
+TMAC_KERNEL_HEADV = 3
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
