@@ -23,7 +23,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "lib")
-PARITY_LIB = os.path.join(LIB_DIR, "libtmac_oracle.so")
+PARITY_LIB = os.environ.get("TMAC_ORACLE_LIB") or os.path.join(LIB_DIR, "libtmac_oracle.so")  # the sanitizer build in tests/test_sanitize.py
 TIMING_LIB = os.path.join(LIB_DIR, "libtmac_oracle_o3.so")
 
 # Compiler flags of the two builds (oracle/Makefile; a CPU test keeps the two in step).

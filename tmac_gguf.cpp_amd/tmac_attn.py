@@ -18,7 +18,9 @@ from typing import Optional
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libtmac_attn.so")
+# TMAC_ATTN_LIB selects another build of the same library (the host sanitizer
+# build, lib/libtmac_attn_san.so, in tests/test_sanitize.py).
+LIB_PATH = os.environ.get("TMAC_ATTN_LIB") or os.path.join(HERE, "lib", "libtmac_attn.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "tmac_attn.h")
 
 TMAC_OK = 0
