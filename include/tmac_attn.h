@@ -28,9 +28,20 @@
  *  - A context is used from one host thread at a time, and its launches must
  *    not overlap on several streams (they share the split-KV workspace).
  *  - Cache layout is the reference's: one row per position, row =
- *    [n_kv_head][head_dim] fp32 (tmac_gguf.cpp:200-201).  head_dim must be 64,
- *    as in the reference's flash kernel (kernel_flash_attn.metal:18).
+ *    [n_kv_head][head_dim] fp32 (tmac_gguf.cpp:200-201).
  *    Query head h reads kv head h / (n_head / n_kv_head) (tmac_gguf.cpp:1099).
+ *  - Shapes.  head_dim 64 with n_head / n_kv_head = G and n_kv_head = KV in
+ *    (G, KV) = (7, 2) (Qwen2-0.5B), (1, 1), (1, 2), (2, 2), (4, 2), (4, 4), (8, 1)
+ *    run the compiled kernels on every entry point.  Like the reference's
+ *    attention_op, which sends head_dim != 64 to kernel_attn (any group, any
+ *    head_dim; metal_backend.hpp:416-452, kernel_attn.metal:7-60), the fp32
+ *    entry points tmac_attention_op, tmac_attention_decode_batched /
+ *    _ragged / _ragged_noalloc and tmac_layer_attention[_devpos] take any
+ *    other n_head a multiple of n_kv_head and any even head_dim up to 256
+ *    (one workgroup per query head; scores scaled by 1/sqrt(head_dim)), and
+ *    tmac_rope_op / tmac_rope_rows any even head_dim up to 256 (kernel_rope.metal:5-22).
+ *    The bf16 / fp16 / Q8_0 caches, the paged caches and chunked prefill keep
+ *    head_dim 64 and the compiled groups; other shapes return TMAC_ERR_UNSUPPORTED.
  */
 #ifndef TMAC_ATTN_H
 #define TMAC_ATTN_H
@@ -49,7 +60,7 @@ enum tmac_status {
     TMAC_ERR_INVALID_ARG = 1,     /* bad shape or value (negative past_len, n_head % n_kv_head, ...) */
     TMAC_ERR_NULL_POINTER = 2,
     TMAC_ERR_MISALIGNED = 3,      /* q/k/v/out/cache rows must be 16-byte aligned */
-    TMAC_ERR_UNSUPPORTED = 4,     /* head_dim != 64, unsupported GQA group, elem_op op 1 */
+    TMAC_ERR_UNSUPPORTED = 4,     /* shape outside an entry point's domain (see Shapes), elem_op op 1 */
     TMAC_ERR_CAPACITY = 5,        /* position beyond the cache / RoPE table / workspace */
     TMAC_ERR_NOT_INITIALIZED = 6,
     TMAC_ERR_CAPTURE = 7,         /* needs an allocation while the stream is being captured */

@@ -22,6 +22,8 @@ constexpr int kHeadPrefetchDepth = 2;
 constexpr int kHvWaves = 8;         // split-V head kernel (short contexts): 512 threads
 constexpr int kHvDepth = 2;         // split-V head kernel: steps of K/V in flight per wave
 constexpr int kHvSplitDefault = 8;  // workgroups per query head, each accumulating 64/8 dims of V
+constexpr int kAnyWavesHost = 8;    // any-shape decode kernel (shapes with no compiled kernel): 512 threads
+constexpr int kAnyMaxDim = 256;     // any-shape kernel and RoPE: even head_dim up to this
 constexpr int kMaxSplits = 256;     // split-KV workgroups per sequence, at most
 constexpr int kPartialStride = kHeadDim + 2;  // per (split, head): acc[64], m, l
 
@@ -65,6 +67,9 @@ struct DecodeArgs {
     // and the launch's max_len (longer sequences give NaN and error bit 1)
     int32_t* seg_meta;
     int sk_max_len;
+    // any-shape kernel (shapes without a compiled kernel): runtime kv heads and head_dim
+    int n_kv_head;
+    int head_dim;
 };
 
 // Chunked causal prefill: query i of sequence s sits at absolute position
@@ -96,8 +101,8 @@ constexpr int kPrefillStageTiles = 4;           // tiles per LDS stage (two per 
 constexpr int kPrefillWaves = 8;     // waves per workgroup: 4 head pairs x 2 stage halves
 
 struct RopeArgs {
-    float* x;                // n_rows rows of [n_heads][64], rotated in place; row r at x + r * row_stride
-    const float2* rope_cs;   // [rope_rows][32]
+    float* x;                // n_rows rows of [n_heads][head_dim], rotated in place; row r at x + r * row_stride
+    const float2* rope_cs;   // [rope_rows][head_dim / 2]
     const int* pos_dev;      // position of row 0 (device; null: pos_host); row r sits at position + r
     int pos_host;
     int n_heads;
@@ -105,6 +110,7 @@ struct RopeArgs {
     int* err;
     int n_rows;
     int64_t row_stride;      // floats between rows
+    int head_dim;            // even; cos/sin table rows hold head_dim / 2 pairs
 };
 
 struct CopyArgs {

@@ -1574,6 +1574,203 @@ __device__ __forceinline__ void combine_sk_body(const DecodeArgs& a) {
         decode_body<T, G, KV, kGroupWaves, DEPTH, kPagedLayer, false>(a);                              \
     }
 
+// Decode for any shape the compiled kernels do not cover ("any-shape" kernel;
+// fp32 caches): runtime n_head, n_kv_head (n_head a multiple of it) and any
+// even head_dim up to kAnyMaxDim, as the reference's kernel_attn accepts any
+// group and head_dim (kernel_attn.metal:7-60, chosen by attention_op when
+// head_dim != 64, metal_backend.hpp:416-452).  grid = (query head, sequence),
+// one split, kAnyWaves waves.  A wave step covers 2 rows: lanes 0..31 one
+// row, lanes 32..63 the next; lane c of a half holds dims c, c + 32, ...
+// (4-byte loads, 128 contiguous bytes per row per load).  q.k is summed over
+// the 32 lanes of a half; the online softmax keeps one running max per wave
+// (raised when a score exceeds it by kTau); waves merge through LDS.
+// Scores use 1/sqrt(head_dim) (tmac_gguf.cpp:1112 for head_dim 64).  Layer
+// mode: q and k_new rotated at pos (RoPE pairs (d, d+1) sit in adjacent
+// lanes), the group's first head stores row pos, wave 0 attends it.
+constexpr int kAnyWaves = kAnyWavesHost;
+constexpr int kAnyDpl = kAnyMaxDim / 32;  // dims per lane at most
+
+__device__ __forceinline__ float half_sum(float x) {  // sum over the 32 lanes of a half wave
+    x = slot_sum(x);
+    x += dpp<0x140>(x);  // row_mirror
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+
+__device__ __forceinline__ float other_half(float x) {  // the value of lane l ^ 32
+    // The swap returns {lanes 0..31 in both halves, lanes 32..63 in both halves}.
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? b[0] : b[1]);
+}
+
+template <int MODE>
+__device__ __forceinline__ void any_body(const DecodeArgs& a) {
+    static_assert(MODE == kUniform || MODE == kRagged || MODE == kLayer, "any-shape kernel modes");
+    constexpr int NW = kAnyWaves;
+    const int hd = a.head_dim, n_head = a.n_head, n_kv = a.n_kv_head;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = lane >> 5, c = lane & 31;
+    const int head = blockIdx.x, seq = blockIdx.y;
+    const int kvh = head / (n_head / n_kv);
+    const int ndim = (hd - c + 31) / 32;  // dims of this lane: c + 32 j, j < ndim
+    const size_t rowf = (size_t)n_kv * hd;  // floats per cache row
+
+    float q[kAnyDpl];
+#pragma unroll
+    for (int j = 0; j < kAnyDpl; ++j) q[j] = j < ndim ? a.q[((size_t)seq * n_head + head) * hd + c + 32 * j] : 0.f;
+    size_t base = 0;
+    int n_pos, pos = 0;
+    if (MODE == kUniform) {
+        base = (size_t)seq * (size_t)a.seq_stride;
+        n_pos = a.n_pos;
+    } else if (MODE == kRagged) {
+        base = (size_t)a.offsets[seq];
+        n_pos = a.lengths[seq];
+    } else {
+        pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+        if (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) {
+            if (head == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
+            return;
+        }
+        n_pos = pos + 1;
+    }
+    n_pos = __builtin_amdgcn_readfirstlane(n_pos);
+    pos = __builtin_amdgcn_readfirstlane(pos);
+    float* out_head = a.out + ((size_t)seq * n_head + head) * hd;
+    if (n_pos <= 0) {
+        for (int i = threadIdx.x; i < hd; i += NW * 64) out_head[i] = 0.f;
+        return;
+    }
+    if (MODE == kRagged && n_pos > a.split_len) {
+        for (int i = threadIdx.x; i < hd; i += NW * 64) out_head[i] = __builtin_nanf("");
+        if (threadIdx.x == 0) atomicOr(a.err, 2);
+        return;
+    }
+    const int mem_rows = MODE == kLayer ? pos : n_pos;
+    const float2* cs_row = nullptr;
+    if (MODE == kLayer) {  // RoPE of q: the pair partner of dim c + 32 j is lane c ^ 1
+        cs_row = a.rope_cs + (size_t)pos * (hd / 2);
+#pragma unroll
+        for (int j = 0; j < kAnyDpl; ++j) {
+            const float xp = dpp<0xB1>(q[j]);
+            if (j < ndim) {
+                const int d = c + 32 * j;
+                const float2 cs = cs_row[d >> 1];
+                float x0 = (d & 1) ? xp : q[j], x1 = (d & 1) ? q[j] : xp;
+                rotate_pair(x0, x1, cs.x, cs.y);
+                q[j] = (d & 1) ? x1 : x0;
+            }
+        }
+    }
+    const float qscale = 1.4426950408889634f / sqrtf((float)hd);  // log2(e) / sqrt(head_dim)
+#pragma unroll
+    for (int j = 0; j < kAnyDpl; ++j) q[j] *= qscale;
+
+    const float* kb = a.k + base * rowf + (size_t)kvh * hd + c;
+    const float* vb = a.v + base * rowf + (size_t)kvh * hd + c;
+    float m = kNegInf, l = 0.f, acc[kAnyDpl];
+#pragma unroll
+    for (int j = 0; j < kAnyDpl; ++j) acc[j] = 0.f;
+    auto attend_row = [&](const float (&kr)[kAnyDpl], const float (&vr)[kAnyDpl], bool valid) {
+        float sc = 0.f;
+#pragma unroll
+        for (int j = 0; j < kAnyDpl; ++j) sc = fmaf(q[j], kr[j], sc);
+        sc = half_sum(sc);
+        sc = valid ? sc : kNegInf;
+        float mx = fmaxf(sc, other_half(sc));
+        if (__any(mx - m > kTau)) {
+            const float mn = fmaxf(m, mx);
+            const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
+            l *= alpha;
+#pragma unroll
+            for (int j = 0; j < kAnyDpl; ++j) acc[j] *= alpha;
+            m = mn;
+        }
+        const float e = fast_exp2(sc - m);
+        l += e;
+#pragma unroll
+        for (int j = 0; j < kAnyDpl; ++j) acc[j] = fmaf(e, valid ? vr[j] : 0.f, acc[j]);
+    };
+    // wave w takes 2-row steps w, w + NW, ...; two steps of K/V in flight
+    const int n_steps = (mem_rows + 1) / 2;
+    float k0[kAnyDpl], v0[kAnyDpl], k1[kAnyDpl], v1[kAnyDpl];
+    auto load_step = [&](float (&kx)[kAnyDpl], float (&vx)[kAnyDpl], int st) {
+        const int r = min(2 * st + half, mem_rows - 1);
+#pragma unroll
+        for (int j = 0; j < kAnyDpl; ++j) {
+            kx[j] = j < ndim ? kb[(size_t)r * rowf + 32 * j] : 0.f;
+            vx[j] = j < ndim ? vb[(size_t)r * rowf + 32 * j] : 0.f;
+        }
+    };
+    int st = wave;
+    if (st < n_steps) load_step(k0, v0, st);
+    for (; st < n_steps; st += 2 * NW) {
+        if (st + NW < n_steps) load_step(k1, v1, st + NW);
+        attend_row(k0, v0, 2 * st + half < mem_rows);
+        if (st + NW >= n_steps) break;
+        if (st + 2 * NW < n_steps) load_step(k0, v0, st + 2 * NW);
+        attend_row(k1, v1, 2 * (st + NW) + half < mem_rows);
+    }
+    if (MODE == kLayer && wave == 0) {  // the new token, lanes 0..31
+        float kn[kAnyDpl], vn[kAnyDpl];
+#pragma unroll
+        for (int j = 0; j < kAnyDpl; ++j) {
+            kn[j] = j < ndim ? a.k_new[(size_t)kvh * hd + c + 32 * j] : 0.f;
+            vn[j] = j < ndim ? a.v_new[(size_t)kvh * hd + c + 32 * j] : 0.f;
+            const float xp = dpp<0xB1>(kn[j]);
+            if (j < ndim) {
+                const int d = c + 32 * j;
+                const float2 cs = cs_row[d >> 1];
+                float x0 = (d & 1) ? xp : kn[j], x1 = (d & 1) ? kn[j] : xp;
+                rotate_pair(x0, x1, cs.x, cs.y);
+                kn[j] = (d & 1) ? x1 : x0;
+                if (half == 0 && head % (n_head / n_kv) == 0) {
+                    a.k_out[(size_t)pos * rowf + (size_t)kvh * hd + d] = kn[j];
+                    a.v_out[(size_t)pos * rowf + (size_t)kvh * hd + d] = vn[j];
+                }
+            }
+        }
+        attend_row(kn, vn, half == 0);
+    }
+    // halves -> wave (same max), waves -> LDS
+    l += other_half(l);
+#pragma unroll
+    for (int j = 0; j < kAnyDpl; ++j) acc[j] += other_half(acc[j]);
+    __shared__ float s_acc[NW][kAnyMaxDim];
+    __shared__ float s_ml[NW][2];
+    if (half == 0) {
+#pragma unroll
+        for (int j = 0; j < kAnyDpl; ++j)
+            if (j < ndim) s_acc[wave][c + 32 * j] = acc[j];
+        if (c == 0) {
+            s_ml[wave][0] = m;
+            s_ml[wave][1] = l;
+        }
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += NW * 64) {
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, s_ml[w][0]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = s_ml[w][0];
+            const float sc = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);
+            L = fmaf(s_ml[w][1], sc, L);
+            A = fmaf(s_acc[w][d], sc, A);
+        }
+        out_head[d] = A / L;
+    }
+}
+
+#if TMAC_IN_PART(0)
+extern "C" __global__ __launch_bounds__(kAnyWaves * 64) void tmac_decode_u_any(DecodeArgs a) { any_body<kUniform>(a); }
+extern "C" __global__ __launch_bounds__(kAnyWaves * 64) void tmac_decode_r_any(DecodeArgs a) { any_body<kRagged>(a); }
+extern "C" __global__ __launch_bounds__(kAnyWaves * 64) void tmac_layer_any(DecodeArgs a) { any_body<kLayer>(a); }
+#endif
+
 #if TMAC_IN_PART(0)
 #define TMAC_DECODE_F32(G, KV)                       \
     TMAC_MODE_KERNELS(G, KV, decode_u, kUniform)      \
@@ -2836,7 +3033,8 @@ extern "C" __global__ __launch_bounds__(kQkvWaves * 64) void tmac_qkv(QkvArgs a)
 // tensor, i.e. what rope_op (metal_backend.hpp:381) dispatches.
 extern "C" __global__ __launch_bounds__(256) void tmac_rope(RopeArgs a) {
     const int gid = blockIdx.x * blockDim.x + threadIdx.x;
-    const int per_row = a.n_heads * (kHeadDim / 2);
+    const int pairs = a.head_dim / 2;
+    const int per_row = a.n_heads * pairs;
     const int row = gid / per_row, rem = gid - row * per_row;
     if (row >= a.n_rows) return;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos_host) + row;
@@ -2844,9 +3042,9 @@ extern "C" __global__ __launch_bounds__(256) void tmac_rope(RopeArgs a) {
         if (rem == 0) atomicOr(a.err, 1);
         return;
     }
-    const int head = rem >> 5, pair = rem & 31;
-    const float2 t = a.rope_cs[(size_t)pos * (kHeadDim / 2) + pair];
-    float2* p = reinterpret_cast<float2*>(a.x + (size_t)row * a.row_stride + head * kHeadDim) + pair;
+    const int head = rem / pairs, pair = rem - head * pairs;
+    const float2 t = a.rope_cs[(size_t)pos * pairs + pair];
+    float2* p = reinterpret_cast<float2*>(a.x + (size_t)row * a.row_stride + (size_t)head * a.head_dim) + pair;
     float2 x = *p;
     rotate_pair(x.x, x.y, t.x, t.y);
     *p = x;

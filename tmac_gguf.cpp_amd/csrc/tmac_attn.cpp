@@ -49,6 +49,7 @@ using tmac::QkvArgs;
 using tmac::kQkvWaves;
 using tmac::RopeArgs;
 using tmac::kHeadDim;
+using tmac::kAnyMaxDim;
 using tmac::kPartialStride;
 using tmac::kGroupWaves;
 using tmac::kHeadWaves;
@@ -119,6 +120,7 @@ struct tmac_context {
     std::map<std::pair<int, int>, hipFunction_t> mdecode[kNarrowTypes][5];
     std::map<std::pair<int, int>, hipFunction_t> prefill;     // chunked prefill, (G, KV)
     std::map<int, hipFunction_t> prefill_pack[2][4];          // prefill tile packing: [paged][cache type], by KV
+    hipFunction_t any[3] = {};  // any-shape decode kernel by mode (shapes with no compiled kernel)
     hipFunction_t k_rope = nullptr, k_copy = nullptr, k_pos = nullptr, k_qkv = nullptr, k_cvt16 = nullptr,
                   k_kq = nullptr, k_cvt_q8 = nullptr;
     float* ws = nullptr;
@@ -202,6 +204,7 @@ bool capturing(hipStream_t s) {
 struct Kernels {
     hipFunction_t group = nullptr, head = nullptr, combine = nullptr;
     hipFunction_t hv = nullptr;      // short-context split-V head kernel (fp32 caches, not paged)
+    hipFunction_t any = nullptr;     // any-shape kernel: a shape with no compiled kernel (fp32, not paged)
     int hv_split = 1;
     hipFunction_t group4 = nullptr;  // 4-wave group kernel when the size is chosen per call (fp32 caches)
     int head_waves = 16;
@@ -217,16 +220,29 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
     if (dt != TMAC_KV_F32 && dt != TMAC_KV_BF16 && dt != TMAC_KV_F16 && dt != TMAC_KV_Q8_0)
         return fail(ctx, TMAC_ERR_INVALID_ARG,
                     "kv_dtype must be TMAC_KV_F32, TMAC_KV_BF16, TMAC_KV_F16 or TMAC_KV_Q8_0");
-    if (head_dim != kHeadDim)
-        return fail(ctx, TMAC_ERR_UNSUPPORTED, "head_dim must be 64 (got " + std::to_string(head_dim) + ")");
     if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head != 0)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "n_head must be a positive multiple of n_kv_head");
     const int g = n_head / n_kv_head;
     auto it = ctx->decode[mode].find({g, n_kv_head});
-    if (it == ctx->decode[mode].end())
+    if (head_dim != kHeadDim || it == ctx->decode[mode].end()) {
+        // No compiled kernel for the shape: fp32, unpaged caches take the any-shape kernel (the
+        // reference's kernel_attn fallback: any group, head_dim even and at most kAnyMaxDim here).
+        if (dt == TMAC_KV_F32 && paged < 0 && head_dim >= 2 && head_dim <= kAnyMaxDim && head_dim % 2 == 0) {
+            if (k) {
+                *k = Kernels{};
+                k->any = ctx->any[mode];
+            }
+            return TMAC_OK;
+        }
+        if (head_dim != kHeadDim)
+            return fail(ctx, TMAC_ERR_UNSUPPORTED,
+                        "head_dim " + std::to_string(head_dim) +
+                            ": only 64 on this entry point and cache type (fp32 attention, layer and batched "
+                            "decode also take even head_dim up to 256)");
         return fail(ctx, TMAC_ERR_UNSUPPORTED,
                     "no kernel for n_head/n_kv_head = " + std::to_string(g) + ", n_kv_head = " +
-                        std::to_string(n_kv_head));
+                        std::to_string(n_kv_head) + " on this entry point and cache type");
+    }
     if (k) {
         k->group_waves = ctx->opt_group_waves == 4 ? 4 : 8;
         k->group = k->group_waves == 4 ? ctx->decode4[mode].at({g, n_kv_head}) : it->second;
@@ -462,6 +478,13 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
     a.blocked = (int)ctx->opt_blocked;
     a.err = ctx->err;
     if (n_seq > 65535) return fail(ctx, TMAC_ERR_INVALID_ARG, "n_seq exceeds 65535");
+    if (k.any) {  // one workgroup per (query head, sequence), no split
+        a.split_len = grid_rows;
+        a.n_splits = 1;
+        a.ws = nullptr;
+        a.n_kv_head = n_kv_head;
+        return launch(ctx, k.any, (unsigned)a.n_head, (unsigned)n_seq, tmac::kAnyWavesHost * 64, stream, &a);
+    }
     const bool unit_grid = a.lengths || a.positions;  // ragged and paged modes
     if (k.head && use_head_kernel(ctx, n_seq, a.n_head, grid_rows)) {
         a.split_len = grid_rows;
@@ -772,6 +795,12 @@ int tmac_init(tmac_context** out, int device) {
             }
         }
     }
+    {
+        const char* any_name[3] = {"tmac_decode_u_any", "tmac_decode_r_any", "tmac_layer_any"};
+        for (int m = 0; m < 3; m++)
+            if ((e = get_function(ctx, &ctx->any[m], any_name[m])) != hipSuccess)
+                return bail(hip_fail(ctx, e, any_name[m]));
+    }
     if ((e = get_function(ctx, &ctx->k_rope, "tmac_rope")) != hipSuccess ||
         (e = get_function(ctx, &ctx->k_copy, "tmac_copy")) != hipSuccess ||
         (e = get_function(ctx, &ctx->k_pos, "tmac_pos_update")) != hipSuccess ||
@@ -829,6 +858,7 @@ int tmac_attention_op(tmac_context* ctx, tmac_stream stream, const float* q, con
     a.seq_stride = 0;
     a.n_pos = past_len + 1;
     a.n_head = n_head;
+    a.head_dim = head_dim;
     return run_decode(ctx, (hipStream_t)stream, kern, a, 1, past_len + 1, n_kv_head);
 }
 
@@ -854,6 +884,7 @@ static int decode_batched_impl(tmac_context* ctx, tmac_stream stream, int dt, co
     a.seq_stride = seq_stride;
     a.n_pos = n_pos;
     a.n_head = n_head;
+    a.head_dim = head_dim;
     return run_decode(ctx, (hipStream_t)stream, kern, a, n_seq, n_pos, n_kv_head);
 }
 
@@ -894,8 +925,9 @@ static int decode_ragged_impl(tmac_context* ctx, tmac_stream stream, int dt, con
     a.offsets = offsets;
     a.lengths = lengths;
     a.n_head = n_head;
+    a.head_dim = head_dim;
     unsigned threads = 0;
-    if (ctx->opt_kernel != TMAC_KERNEL_HEAD && !use_head_kernel(ctx, n_seq, n_head, max_len)) {
+    if (!kern.any && ctx->opt_kernel != TMAC_KERNEL_HEAD && !use_head_kernel(ctx, n_seq, n_head, max_len)) {
         if (hipFunction_t sk = stream_k_kernel(ctx, dt, false, n_seq, n_head, n_kv_head, &threads))
             return run_decode_sk(ctx, (hipStream_t)stream, sk, threads,
                                  ctx->combine_sk.at({n_head / n_kv_head, n_kv_head}), a, n_seq, max_len);
@@ -966,6 +998,7 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
     a.pos_dev = pos_dev;
     a.pos_host = pos;
     a.capacity = capacity;
+    a.head_dim = head_dim;
     return run_decode(ctx, stream, kern, a, 1, pos_dev ? capacity : pos + 1, n_kv_head);
 }
 
@@ -1133,6 +1166,7 @@ static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const flo
     if (!q || !k_cache || !v_cache || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "prefill: null buffer");
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
         return fail(ctx, TMAC_ERR_MISALIGNED, "prefill: buffers must be 16-byte aligned");
+    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "prefill: head_dim must be 64");
     if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, nullptr, kModeUniform))) return rc;
     if (n_seq < 0 || n_q < 0 || prefix_len < 0 || (int64_t)prefix_len + n_q > INT_MAX)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill: need n_seq, n_q, prefix_len >= 0");
@@ -1205,7 +1239,8 @@ int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int val
 int tmac_rope_prepare(tmac_context* ctx, int head_dim, float base, int n_pos) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
-    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope: head_dim must be 64");
+    if (head_dim < 2 || head_dim > kAnyMaxDim || head_dim % 2)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope: head_dim must be even, 2..256");
     if (n_pos < 1 || !(base > 0.f) || !std::isfinite(base))
         return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_prepare: need n_pos >= 1 and base > 0");
     if ((rc = set_device(ctx))) return rc;
@@ -1219,15 +1254,16 @@ int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads
     if (rc) return rc;
     if (!data) return fail(ctx, TMAC_ERR_NULL_POINTER, "rope_op: null data");
     if (!aligned16(data)) return fail(ctx, TMAC_ERR_MISALIGNED, "rope_op: data must be 16-byte aligned");
-    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope_op: head_dim must be 64");
+    if (head_dim < 2 || head_dim > kAnyMaxDim || head_dim % 2)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope_op: head_dim must be even, 2..256");
     if (n_heads < 0 || pos < 0 || pos == INT_MAX) return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_op: bad n_heads/pos");
     if (!(base > 0.f) || !std::isfinite(base)) return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_op: bad base");
     if (n_heads == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
     const RopeTable* rt = nullptr;
     if ((rc = rope_table(ctx, (hipStream_t)stream, head_dim, base, pos + 1, &rt))) return rc;
-    RopeArgs a{data, rt->dev, nullptr, pos, n_heads, rt->rows, ctx->err, 1, 0};
-    const int threads = n_heads * (kHeadDim / 2);
+    RopeArgs a{data, rt->dev, nullptr, pos, n_heads, rt->rows, ctx->err, 1, 0, head_dim};
+    const int threads = n_heads * (head_dim / 2);
     return launch(ctx, ctx->k_rope, (unsigned)((threads + 255) / 256), 1, 256, (hipStream_t)stream, &a);
 }
 
@@ -1238,18 +1274,19 @@ int tmac_rope_rows(tmac_context* ctx, tmac_stream stream, float* data, int n_row
     if (!data) return fail(ctx, TMAC_ERR_NULL_POINTER, "rope_rows: null data");
     if (!aligned16(data) || row_stride % 4 != 0)
         return fail(ctx, TMAC_ERR_MISALIGNED, "rope_rows: data and rows must be 16-byte aligned");
-    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope_rows: head_dim must be 64");
+    if (head_dim < 2 || head_dim > kAnyMaxDim || head_dim % 2)
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "rope_rows: head_dim must be even, 2..256");
     if (n_rows < 0 || n_heads < 0 || first_pos < 0 || (int64_t)first_pos + n_rows > INT_MAX ||
-        (n_rows > 1 && row_stride < (int64_t)n_heads * kHeadDim) ||
-        (int64_t)n_rows * n_heads * (kHeadDim / 2) > INT_MAX)
+        (n_rows > 1 && row_stride < (int64_t)n_heads * head_dim) ||
+        (int64_t)n_rows * n_heads * (head_dim / 2) > INT_MAX)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_rows: bad n_rows / row_stride / n_heads / first_pos");
     if (!(base > 0.f) || !std::isfinite(base)) return fail(ctx, TMAC_ERR_INVALID_ARG, "rope_rows: bad base");
     if (n_rows == 0 || n_heads == 0) return TMAC_OK;
     if ((rc = set_device(ctx))) return rc;
     const RopeTable* rt = nullptr;
     if ((rc = rope_table(ctx, (hipStream_t)stream, head_dim, base, first_pos + n_rows, &rt))) return rc;
-    RopeArgs a{data, rt->dev, nullptr, first_pos, n_heads, rt->rows, ctx->err, n_rows, row_stride};
-    const int64_t threads = (int64_t)n_rows * n_heads * (kHeadDim / 2);
+    RopeArgs a{data, rt->dev, nullptr, first_pos, n_heads, rt->rows, ctx->err, n_rows, row_stride, head_dim};
+    const int64_t threads = (int64_t)n_rows * n_heads * (head_dim / 2);
     return launch(ctx, ctx->k_rope, (unsigned)((threads + 255) / 256), 1, 256, (hipStream_t)stream, &a);
 }
 
@@ -1407,9 +1444,10 @@ int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if (!split_len || !n_splits) return TMAC_ERR_NULL_POINTER;
-    if ((rc = check_shape(ctx, n_head, n_kv_head, kHeadDim, nullptr, kModeUniform))) return rc;
+    Kernels kern;
+    if ((rc = check_shape(ctx, n_head, n_kv_head, kHeadDim, &kern, kModeUniform))) return rc;
     if (n_seq < 1 || n_pos < 1) return fail(ctx, TMAC_ERR_INVALID_ARG, "query_split: n_seq, n_pos >= 1");
-    if (use_head_kernel(ctx, n_seq, n_head, n_pos)) {
+    if (kern.any || use_head_kernel(ctx, n_seq, n_head, n_pos)) {
         *split_len = n_pos;
         *n_splits = 0;  // 0 = head kernel (one workgroup per query head)
         return TMAC_OK;
