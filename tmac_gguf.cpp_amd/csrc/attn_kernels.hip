@@ -2454,16 +2454,31 @@ __device__ __forceinline__ u32x2 i8x4_to_bf16(unsigned w) {
                  __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u)};
 }
 
+// Four int8 (one word) -> four fp16 (two words, element 2i in the low half),
+// exactly: byte b becomes u = b ^ 0x80 = b + 128, the fp16 with bits
+// 0x6400 | u is 1024 + u, and subtracting 1152 (packed) leaves b.
+__device__ __forceinline__ u32x2 i8x4_to_f16(unsigned w) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const unsigned x = w ^ 0x80808080u;
+    const unsigned a = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // bytes u0, 0x64, u1, 0x64
+    const unsigned b = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);  // bytes u2, 0x64, u3, 0x64
+    const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    return u32x2{__builtin_bit_cast(unsigned, __builtin_bit_cast(f16x2, a) - bias),
+                 __builtin_bit_cast(unsigned, __builtin_bit_cast(f16x2, b) - bias)};
+}
+
 // Element type -> MFMA operand type, tile, and cache row bytes.
 template <typename T, int KV>
 struct MTraits {
     using Ops = MMath<T>;
+    using QOps = MMath<T>;
     using Tile = MTile<T, KV>;
     static constexpr int kCacheRowBytes = Tile::ROWB;
 };
 template <int KV>
 struct MTraits<q8_0_t, KV> {
     using Ops = MMath<__bf16>;
+    using QOps = MMath<_Float16>;
     using Tile = MTileQ8<KV>;
     static constexpr int kCacheRowBytes = Tile::ROWB;
 };
@@ -2489,6 +2504,9 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     constexpr bool Q8 = __is_same(T, q8_0_t);
     using Tile = typename MTraits<T, KV>::Tile;
     using M = typename MTraits<T, KV>::Ops;
+    // q . k operand type: the cache's 16-bit type; Q8_0 keys are widened to fp16
+    // (exact, i8x4_to_f16), its p . v stays on bf16.
+    using MQ = typename MTraits<T, KV>::QOps;
     constexpr int ROWC = MTraits<T, KV>::kCacheRowBytes;  // cache bytes per row
     constexpr int ROWB = KV * kHeadDim * 2;                // bytes per row of the 16-bit LDS V tile
     constexpr int CPR = ROWB / 16, NKB = 2 * KV, NMB = 4 * KV;
@@ -2526,7 +2544,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
         for (int t = 0; t < 8; ++t) qx[b][t] = mine ? x[t] * a.qscale : 0.f;
     }
     float s_unscale = 1.0f;  // S^T column scale to undo (fp16)
-    if (M::kScaleQ) {
+    if (MQ::kScaleQ) {
         float mx = 0.f;
 #pragma unroll
         for (int b = 0; b < NKB; ++b)
@@ -2542,7 +2560,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             for (int t = 0; t < 8; ++t) qx[b][t] = __builtin_ldexpf(qx[b][t], qe);
         s_unscale = __builtin_ldexpf(1.0f, -qe);
     }
-    typename M::v8 qpart[3][NKB];
+    typename MQ::v8 qpart[3][NKB];
 #pragma unroll
     for (int b = 0; b < NKB; ++b) {
         u32x4 w[3];
@@ -2551,13 +2569,13 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             float e0 = qx[b][2 * t], e1 = qx[b][2 * t + 1];
 #pragma unroll
             for (int part = 0; part < 3; ++part) {
-                w[part][t] = M::pack2(e0, e1);
-                e0 -= M::lo(w[part][t]);  // exact
-                e1 -= M::hi(w[part][t]);
+                w[part][t] = MQ::pack2(e0, e1);
+                e0 -= MQ::lo(w[part][t]);  // exact
+                e1 -= MQ::hi(w[part][t]);
             }
         }
 #pragma unroll
-        for (int part = 0; part < 3; ++part) qpart[part][b] = __builtin_bit_cast(typename M::v8, w[part]);
+        for (int part = 0; part < 3; ++part) qpart[part][b] = __builtin_bit_cast(typename MQ::v8, w[part]);
     }
 
     // LDS: during the tile loop each wave owns a V tile (16-bit, swizzled) and,
@@ -2616,7 +2634,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     // (Q8_0: the raw tile is already in LDS when t is null).
     auto compute = [&](const Tile* t, int valid) {
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-        float dv[NKB][4];  // Q8_0: V scale of block b for this lane's keys 4 g + i
+        float dv[2][4];  // Q8_0: V scale of 32-dim block b (own kv head) for this lane's keys 4 g + i
         if constexpr (Q8) {
             constexpr int RB = MTileQ8<KV>::ROWB;
             if (t) {
@@ -2637,33 +2655,38 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
                 *reinterpret_cast<u32x4*>(sv + wr_off[2 * i]) = w0;
                 *reinterpret_cast<u32x4*>(sv + wr_off[2 * i + 1]) = w1;
             }
-            float dk[NKB][4];
+            // Scales of this lane's keys 4 g + i in its own column's kv head only:
+            // the other kv head's S^T entries of the column are exactly 0 (its
+            // query operand is 0 there), and its P' is never read back.
+            const int kvc = min(col, NH - 1) / G;
+            float dk[2][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int h = 0; h < KV; ++h) {
-                    const int o = (4 * g + i) * RB + h * kQ8HeadBytes + 64;
-                    const bool ok = 4 * g + i < valid;  // rows past the tile's end: weight 0, whatever LDS holds
-                    const unsigned kw = *reinterpret_cast<const unsigned*>(rk + o);
-                    const unsigned vw = ok ? *reinterpret_cast<const unsigned*>(rv + o) : 0u;
-                    dk[2 * h][i] = half_bits_to_float(kw & 0xffffu);
-                    dk[2 * h + 1][i] = half_bits_to_float(kw >> 16);
-                    dv[2 * h][i] = half_bits_to_float(vw & 0xffffu);
-                    dv[2 * h + 1][i] = half_bits_to_float(vw >> 16);
-                }
+            for (int i = 0; i < 4; ++i) {
+                const int o = (4 * g + i) * RB + kvc * kQ8HeadBytes + 64;
+                const bool ok = 4 * g + i < valid;  // rows past the tile's end: weight 0, whatever LDS holds
+                const unsigned kw = *reinterpret_cast<const unsigned*>(rk + o);
+                const unsigned vw = ok ? *reinterpret_cast<const unsigned*>(rv + o) : 0u;
+                dk[0][i] = half_bits_to_float(kw & 0xffffu);
+                dk[1][i] = half_bits_to_float(kw >> 16);
+                dv[0][i] = half_bits_to_float(vw & 0xffffu);
+                dv[1][i] = half_bits_to_float(vw >> 16);
+            }
+            // S^T of each 32-dim block parity, both kv heads into one accumulator
+            // (the block-diagonal query keeps them apart): K widened to fp16
+            // exactly, fp16 MFMAs against the fp16 query parts.
+            f32x4 sb[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int b = 0; b < NKB; ++b) {
                 const unsigned* src =
                     reinterpret_cast<const unsigned*>(rk + col * RB + (b / 2) * kQ8HeadBytes + 32 * (b % 2) + 8 * g);
-                const u32x2 k0 = i8x4_to_bf16(src[0]), k1 = i8x4_to_bf16(src[1]);
+                const u32x2 k0 = i8x4_to_f16(src[0]), k1 = i8x4_to_f16(src[1]);
                 const u32x4 kw = {k0[0], k0[1], k1[0], k1[1]};
-                const bf16x8 kop = __builtin_bit_cast(bf16x8, kw);
-                f32x4 sb = f32x4{0.f, 0.f, 0.f, 0.f};
+                const typename MQ::v8 kop = __builtin_bit_cast(typename MQ::v8, kw);
 #pragma unroll
-                for (int part = 2; part >= 0; --part) sb = M::mfma32(kop, qpart[part][b], sb);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s[i] = __builtin_fmaf(dk[b][i], sb[i], s[i]);
+                for (int part = 2; part >= 0; --part) sb[b % 2] = MQ::mfma32(kop, qpart[part][b], sb[b % 2]);
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[i] = __builtin_fmaf(dk[0][i], sb[0][i], dk[1][i] * sb[1][i]);
         } else {
 #pragma unroll
             for (int i = 0; i < NWR; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t->v[i];
@@ -2673,7 +2696,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
                 for (int part = 2; part >= 0; --part)  // smallest part first
                     s = M::mfma32(t->k[b], qpart[part][b], s);
         }
-        if (M::kScaleQ) s *= s_unscale;
+        if (MQ::kScaleQ) s *= s_unscale;
         if (valid < kMTileRows) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -2696,7 +2719,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             l += p[i];
         }
         // P^T (times kPScale; Q8_0: times the key's V scale of the block) as 16-bit hi + lo
-        constexpr int NP = Q8 ? NKB : 1;
+        constexpr int NP = Q8 ? 2 : 1;  // Q8_0: one P' per 32-dim block of the column's own kv head
         typename M::v4 bh[NP], bl[NP];
 #pragma unroll
         for (int b = 0; b < NP; ++b) {
@@ -2717,7 +2740,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
             const typename M::v4 va = M::read_tr(sv + rd_off[mb]);
-            const int b = Q8 ? mb / 2 : 0;  // Q8_0 block of dims 16 mb .. 16 mb + 15
+            const int b = Q8 ? (mb & 3) >> 1 : 0;  // Q8_0: 32-dim block of dims 16 mb .. 16 mb + 15 in its kv head
             acc[mb] = M::mfma16(va, bh[b], acc[mb]);
             acc[mb] = M::mfma16(va, bl[b], acc[mb]);
         }
