@@ -2319,6 +2319,7 @@ struct MMath<__bf16> {
     typedef bf16x8 v8;
     typedef i16x4 v4;
     static constexpr bool kScaleQ = false;
+    static constexpr int kQParts = 3;  // 16-bit parts of an fp32 query element
     static constexpr float kPScale = 1.0f;
     __device__ static unsigned pack2(float a, float b) { return bf16_pair(a, b); }
     __device__ static float lo(unsigned w) { return __uint_as_float(w << 16); }
@@ -2334,6 +2335,7 @@ struct MMath<_Float16> {
     typedef f16x8 v8;
     typedef f16x4 v4;
     static constexpr bool kScaleQ = true;
+    static constexpr int kQParts = 2;
     static constexpr float kPScale = 128.0f;
     __device__ static unsigned pack2(float a, float b) {
         typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -2351,7 +2353,10 @@ struct MMath<_Float16> {
 
 constexpr int kMTileRows = 16;  // positions per tile
 constexpr int kMWaves = kMWavesHost;
-constexpr int kMDepth = 3;      // tiles of K and V in flight per wave
+// Tiles of K and V in flight per wave.  With the tile loop's exact waits, 2
+// beats 3 (3 spills registers for Q8_0 and fp16 caches, and was 0.5% slower
+// for bf16 at config 3).
+constexpr int kMDepth = 2;
 
 template <typename T, int KV>
 struct MTile {
@@ -2406,27 +2411,39 @@ struct MTileQ8 {
     static constexpr int ROWB = KV * kQ8HeadBytes;  // cache bytes per row
     static constexpr int RAW = kMTileRows * ROWB;   // bytes per tensor tile
     static constexpr int NCH = RAW / 16;            // 16-byte chunks per tensor tile
-    static constexpr int NR = (NCH + 63) / 64;      // chunk loads per lane
+    static constexpr int NF = NCH / 64;             // chunk loads per lane and tensor covering 64 chunks
+    static constexpr int REM = NCH % 64;            // chunks left per tensor: K's and V's share one load
+    static_assert(NF >= 1 && REM > 0 && 2 * REM <= 64, "68-byte head rows: 16 KV rows of 4-byte words");
     static constexpr int NKB = 2 * KV;
     static constexpr int NMB = 4 * KV;
     static constexpr int NVU = kMTileRows * KV * 4 / 64;  // 16-value V runs per lane per tile
-    u32x4 k[NR], v[NR];
+    u32x4 k[NF], v[NF];
+    u32x4 x;  // lane e < REM: K chunk 64 NF + e; REM <= e < 2 REM: V chunk 64 NF + e - REM
 };
 
-// A full tile: chunk c = 64 i + lane (the last chunk repeated past the end).
-// K chunks use normal loads (a tile's first and last 128-byte lines are shared
-// with the neighbouring tiles, which other waves read at about the same time:
-// 77 -> 73 us at config 3), V chunks non-temporal loads.
+// Lane `lane`'s chunk of the shared remainder load: (tensor is V, chunk index).
+template <int KV>
+__device__ __forceinline__ int2 q8_rem_chunk(int lane) {
+    using Tile = MTileQ8<KV>;
+    const int e = lane % (2 * Tile::REM);  // lanes past 2 REM repeat the first 2 REM (same lines)
+    return int2{e >= Tile::REM, 64 * Tile::NF + e % Tile::REM};
+}
+
+// A full tile: chunks 64 i + lane of each tensor, then the K and V remainders
+// in one load.  K chunks use normal loads (a tile's first and last 128-byte
+// lines are shared with the neighbouring tiles, which other waves read at
+// about the same time: 77 -> 73 us at config 3), V chunks non-temporal loads.
 template <int KV>
 __device__ __forceinline__ void mtile_load_q8(MTileQ8<KV>& t, const char* __restrict__ kbase,
                                               const char* __restrict__ vbase, int lane) {
     using Tile = MTileQ8<KV>;
 #pragma unroll
-    for (int i = 0; i < Tile::NR; ++i) {
-        const int c = min(64 * i + lane, Tile::NCH - 1);
-        t.k[i] = *reinterpret_cast<const u32x4*>(kbase + 16 * c);  // normal: see mtile_load
-        t.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + 16 * c));
+    for (int i = 0; i < Tile::NF; ++i) {
+        t.k[i] = *reinterpret_cast<const u32x4*>(kbase + 16 * (64 * i + lane));  // normal: see mtile_load
+        t.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + 16 * (64 * i + lane)));
     }
+    const int2 rc = q8_rem_chunk<KV>(lane);
+    t.x = *reinterpret_cast<const u32x4*>((rc.x ? vbase : kbase) + 16 * rc.y);
 }
 
 // A partial tile (valid < 16 rows) straight into the LDS raw areas, word by
@@ -2521,9 +2538,13 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     const float2* cs_row = LAYER ? a.rope_cs + (size_t)pos * (kHeadDim / 2) : nullptr;
 
     // Q^T operands: column col, dims 32 (b % 2) + 8 g + 0..7 of kv head b / 2,
-    // zero unless head col belongs to that kv head.  Three 16-bit parts (hi +
-    // mid + lo), each rounded to nearest from the exact remainder of the
-    // previous ones.  fp16: the column is first scaled by 2^qe (exact).
+    // zero unless head col belongs to that kv head.  16-bit parts, each rounded
+    // to nearest from the exact remainder of the previous ones: bf16 three (hi +
+    // mid + lo, 24 bits: fp32 exactly), fp16 two (22 bits: |q - hi - lo| <=
+    // 2^-22 |q|, below the rounding of fp32 sums of 64 products).  fp16: the
+    // column is first scaled by 2^qe (exact), its largest element into
+    // [2^14, 2^15): an element's error is then at most max(2^-22 |q|, 2^-25),
+    // the second (fp16 subnormal lo parts) below 2^-39 of the largest.
     float qx[NKB][8];
 #pragma unroll
     for (int b = 0; b < NKB; ++b) {
@@ -2560,22 +2581,23 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             for (int t = 0; t < 8; ++t) qx[b][t] = __builtin_ldexpf(qx[b][t], qe);
         s_unscale = __builtin_ldexpf(1.0f, -qe);
     }
-    typename MQ::v8 qpart[3][NKB];
+    constexpr int QP = MQ::kQParts;
+    typename MQ::v8 qpart[QP][NKB];
 #pragma unroll
     for (int b = 0; b < NKB; ++b) {
-        u32x4 w[3];
+        u32x4 w[QP];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             float e0 = qx[b][2 * t], e1 = qx[b][2 * t + 1];
 #pragma unroll
-            for (int part = 0; part < 3; ++part) {
+            for (int part = 0; part < QP; ++part) {
                 w[part][t] = MQ::pack2(e0, e1);
                 e0 -= MQ::lo(w[part][t]);  // exact
                 e1 -= MQ::hi(w[part][t]);
             }
         }
 #pragma unroll
-        for (int part = 0; part < 3; ++part) qpart[part][b] = __builtin_bit_cast(typename MQ::v8, w[part]);
+        for (int part = 0; part < QP; ++part) qpart[part][b] = __builtin_bit_cast(typename MQ::v8, w[part]);
     }
 
     // LDS: during the tile loop each wave owns a V tile (16-bit, swizzled) and,
@@ -2606,6 +2628,11 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     }
     char* rk = sv + VT;    // Q8_0: raw K tile
     char* rv = rk + RAWT;  // Q8_0: raw V tile
+    int x_off = 0;         // Q8_0: this lane's remainder chunk, from rk
+    if constexpr (Q8) {
+        const int2 rc = q8_rem_chunk<KV>(lane);
+        x_off = rc.x * RAWT + 16 * rc.y;
+    }
     int rd_off[NMB];
     {
         const int j = col, r = 4 * g + j / 4;
@@ -2639,11 +2666,11 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             constexpr int RB = MTileQ8<KV>::ROWB;
             if (t) {
 #pragma unroll
-                for (int i = 0; i < MTileQ8<KV>::NR; ++i) {
-                    const int c = min(64 * i + lane, MTileQ8<KV>::NCH - 1);
-                    *reinterpret_cast<u32x4*>(rk + 16 * c) = t->k[i];
-                    *reinterpret_cast<u32x4*>(rv + 16 * c) = t->v[i];
+                for (int i = 0; i < MTileQ8<KV>::NF; ++i) {
+                    *reinterpret_cast<u32x4*>(rk + 16 * (64 * i + lane)) = t->k[i];
+                    *reinterpret_cast<u32x4*>(rv + 16 * (64 * i + lane)) = t->v[i];
                 }
+                if (lane < 2 * MTileQ8<KV>::REM) *reinterpret_cast<u32x4*>(rk + x_off) = t->x;
             }
 #pragma unroll
             for (int i = 0; i < MTileQ8<KV>::NVU; ++i) {  // V runs: widen to bf16, into the V tile
@@ -2683,7 +2710,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
                 const u32x4 kw = {k0[0], k0[1], k1[0], k1[1]};
                 const typename MQ::v8 kop = __builtin_bit_cast(typename MQ::v8, kw);
 #pragma unroll
-                for (int part = 2; part >= 0; --part) sb[b % 2] = MQ::mfma32(kop, qpart[part][b], sb[b % 2]);
+                for (int part = QP - 1; part >= 0; --part) sb[b % 2] = MQ::mfma32(kop, qpart[part][b], sb[b % 2]);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[i] = __builtin_fmaf(dk[0][i], sb[0][i], dk[1][i] * sb[1][i]);
@@ -2693,7 +2720,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
 #pragma unroll
             for (int b = 0; b < NKB; ++b)
 #pragma unroll
-                for (int part = 2; part >= 0; --part)  // smallest part first
+                for (int part = QP - 1; part >= 0; --part)  // smallest part first
                     s = M::mfma32(t->k[b], qpart[part][b], s);
         }
         if (MQ::kScaleQ) s *= s_unscale;
@@ -2750,22 +2777,37 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     const int nk = (full - wave + NW - 1) / NW;  // this wave's full tiles: wave + NW * k
     if (nk > 0) {
         Tile buf[D];
+        auto load = [&](int d, int k) {
+            const size_t off = tile_off(wave + NW * k);
+            mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+        };
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const size_t off = tile_off(wave + NW * min(d, nk - 1));
-            mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
+            load(d, min(d, nk - 1));
             __builtin_amdgcn_sched_barrier(0);
         }
-        for (int k0 = 0; k0 < nk; k0 += D) {
+        // Steady state: every prefetch is one of the wave's tiles, so every
+        // iteration issues the same loads and a tile's compute waits only for
+        // that tile's loads (a conditional prefetch makes the compiler wait
+        // for all loads in flight, the D - 1 newer tiles included).  No tile
+        // is fetched twice (a prefetch clamped to the last tile re-read it).
+        int k0 = 0;
+        for (; k0 + 2 * D <= nk; k0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                if (k0 + d < nk) compute(&buf[d], kMTileRows);
-                if (k0 + d + D < nk) {  // no prefetch past the wave's last tile (1.6% at config 3, bf16)
-                    const size_t off = tile_off(wave + NW * (k0 + d + D));
-                    mtile_load_any<T, KV>(buf[d], kc + off, vc + off, kMTileRows, lane);
-                }
+                compute(&buf[d], kMTileRows);
+                load(d, k0 + d + D);
             }
         }
+        // Drain: the last nk - k0 < 2 D tiles.
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (k0 + d < nk) compute(&buf[d], kMTileRows);
+            if (k0 + d + D < nk) load(d, k0 + d + D);
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (k0 + D + d < nk) compute(&buf[d], kMTileRows);
     }
     const int tail = n_rows - full * kMTileRows;
     if (tail > 0 && (full % NW) == wave) {
