@@ -2301,6 +2301,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_v;
 typedef __attribute__((address_space(3))) bf16x4_v* lds_bf16x4_ptr;
 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 f16x4_v;
@@ -2338,7 +2339,6 @@ struct MMath<_Float16> {
     static constexpr int kQParts = 2;
     static constexpr float kPScale = 128.0f;
     __device__ static unsigned pack2(float a, float b) {
-        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
         const f16x2 v = {(_Float16)a, (_Float16)b};
         return __builtin_bit_cast(unsigned, v);
     }
@@ -2475,7 +2475,6 @@ __device__ __forceinline__ u32x2 i8x4_to_bf16(unsigned w) {
 // exactly: byte b becomes u = b ^ 0x80 = b + 128, the fp16 with bits
 // 0x6400 | u is 1024 + u, and subtracting 1152 (packed) leaves b.
 __device__ __forceinline__ u32x2 i8x4_to_f16(unsigned w) {
-    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     const unsigned x = w ^ 0x80808080u;
     const unsigned a = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // bytes u0, 0x64, u1, 0x64
     const unsigned b = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);  // bytes u2, 0x64, u3, 0x64
@@ -2661,7 +2660,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     // (Q8_0: the raw tile is already in LDS when t is null).
     auto compute = [&](const Tile* t, int valid) {
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-        float dv[2][4];  // Q8_0: V scale of 32-dim block b (own kv head) for this lane's keys 4 g + i
+        f16x2 dv[4];  // Q8_0: V scales (blocks 0, 1 of the own kv head) of this lane's keys 4 g + i
         if constexpr (Q8) {
             constexpr int RB = MTileQ8<KV>::ROWB;
             if (t) {
@@ -2685,18 +2684,18 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             // Scales of this lane's keys 4 g + i in its own column's kv head only:
             // the other kv head's S^T entries of the column are exactly 0 (its
             // query operand is 0 there), and its P' is never read back.
+            // Kept as fp16 pairs: each use is one v_fma_mix_f32 (fp16 operand
+            // selected from either half, no conversion).
             const int kvc = min(col, NH - 1) / G;
-            float dk[2][4];
+            f16x2 dk[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int o = (4 * g + i) * RB + kvc * kQ8HeadBytes + 64;
                 const bool ok = 4 * g + i < valid;  // rows past the tile's end: weight 0, whatever LDS holds
                 const unsigned kw = *reinterpret_cast<const unsigned*>(rk + o);
                 const unsigned vw = ok ? *reinterpret_cast<const unsigned*>(rv + o) : 0u;
-                dk[0][i] = half_bits_to_float(kw & 0xffffu);
-                dk[1][i] = half_bits_to_float(kw >> 16);
-                dv[0][i] = half_bits_to_float(vw & 0xffffu);
-                dv[1][i] = half_bits_to_float(vw >> 16);
+                dk[i] = __builtin_bit_cast(f16x2, kw);
+                dv[i] = __builtin_bit_cast(f16x2, vw);
             }
             // S^T of each 32-dim block parity, both kv heads into one accumulator
             // (the block-diagonal query keeps them apart): K widened to fp16
@@ -2712,8 +2711,11 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
 #pragma unroll
                 for (int part = QP - 1; part >= 0; --part) sb[b % 2] = MQ::mfma32(kop, qpart[part][b], sb[b % 2]);
             }
+            // + 0.0f keeps the product a fused multiply-add (one v_fma_mix_f32
+            // with the fp16 operand) rather than a conversion and a multiply.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s[i] = __builtin_fmaf(dk[0][i], sb[0][i], dk[1][i] * sb[1][i]);
+            for (int i = 0; i < 4; ++i)
+                s[i] = __builtin_fmaf((float)dk[i][0], sb[0][i], __builtin_fmaf((float)dk[i][1], sb[1][i], 0.0f));
         } else {
 #pragma unroll
             for (int i = 0; i < NWR; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t->v[i];
@@ -2723,7 +2725,8 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
                 for (int part = QP - 1; part >= 0; --part)  // smallest part first
                     s = M::mfma32(t->k[b], qpart[part][b], s);
         }
-        if (MQ::kScaleQ) s *= s_unscale;
+        // fp16 queries: s holds S^T times 2^qe; the power of two comes off
+        // the tile max and inside the exp2 argument (exact either way).
         if (valid < kMTileRows) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -2731,6 +2734,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
         }
         float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
         tm = max4_rows(tm);
+        if (MQ::kScaleQ) tm *= s_unscale;
         if (__any(tm - m > kTau)) {  // raise the running max (rare after the first tile)
             const float mn = fmaxf(m, tm);
             const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
@@ -2742,7 +2746,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
         float p[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            p[i] = fast_exp2(s[i] - m);  // 0 for masked keys
+            p[i] = fast_exp2(MQ::kScaleQ ? __builtin_fmaf(s[i], s_unscale, -m) : s[i] - m);  // 0 for masked keys
             l += p[i];
         }
         // P^T (times kPScale; Q8_0: times the key's V scale of the block) as 16-bit hi + lo
@@ -2755,8 +2759,8 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             for (int i = 0; i < 2; ++i) {
                 float p0 = p[2 * i] * M::kPScale, p1 = p[2 * i + 1] * M::kPScale;
                 if constexpr (Q8) {
-                    p0 *= dv[b][2 * i];
-                    p1 *= dv[b][2 * i + 1];
+                    p0 = __builtin_fmaf((float)dv[2 * i][b], p0, 0.0f);
+                    p1 = __builtin_fmaf((float)dv[2 * i + 1][b], p1, 0.0f);
                 }
                 ph[i] = M::pack2(p0, p1);
                 pl[i] = M::pack2(p0 - M::lo(ph[i]), p1 - M::hi(ph[i]));
