@@ -2669,7 +2669,9 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
                     *reinterpret_cast<u32x4*>(rk + 16 * (64 * i + lane)) = t->k[i];
                     *reinterpret_cast<u32x4*>(rv + 16 * (64 * i + lane)) = t->v[i];
                 }
-                if (lane < 2 * MTileQ8<KV>::REM) *reinterpret_cast<u32x4*>(rk + x_off) = t->x;
+                // Lanes past 2 REM hold and store copies of lanes 0 .. 2 REM - 1's
+                // chunks (same address, same bytes): no branch in the tile code.
+                *reinterpret_cast<u32x4*>(rk + x_off) = t->x;
             }
 #pragma unroll
             for (int i = 0; i < MTileQ8<KV>::NVU; ++i) {  // V runs: widen to bf16, into the V tile
@@ -2732,10 +2734,13 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             for (int i = 0; i < 4; ++i)
                 if (4 * g + i >= valid) s[i] = kNegInf;
         }
+        // Every lane tests its own 4 keys: the column's max exceeds m + kTau
+        // exactly when one of its 4 lanes' does, and only then (rare after
+        // the first tile) is the column max reduced over the lanes.
         float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        tm = max4_rows(tm);
         if (MQ::kScaleQ) tm *= s_unscale;
-        if (__any(tm - m > kTau)) {  // raise the running max (rare after the first tile)
+        if (__any(tm - m > kTau)) {  // raise the running max
+            tm = max4_rows(tm);
             const float mn = fmaxf(m, tm);
             const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
             l *= alpha;
