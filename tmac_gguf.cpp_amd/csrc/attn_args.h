@@ -16,7 +16,8 @@ constexpr int kPrefetchDepthQ8 = 8; // the same for Q8_0 caches (136-byte rows a
 constexpr int kQ8HeadBytes = 68;    // Q8_0 cache: one (row, kv head) = int8 q[64] + fp16 d0, d1
 constexpr int kPageRows = 16;       // paged caches: rows per page
 constexpr int kPageShift = 4;       // log2(kPageRows)
-constexpr int kMWavesHost = 8;      // MFMA decode kernel: waves per workgroup
+constexpr int kMWaves16Host = 4;    // MFMA decode kernel, bf16 / fp16 caches: waves per workgroup
+constexpr int kMWavesQ8Host = 8;    // MFMA decode kernel, Q8_0 caches (widening needs 2 waves per SIMD)
 constexpr int kHeadWaves = 16;      // "head" decode kernel (short contexts): 1024 threads
 constexpr int kHeadPrefetchDepth = 2;
 constexpr int kHvWaves = 8;         // split-V head kernel (short contexts): 512 threads

@@ -2352,7 +2352,14 @@ struct MMath<_Float16> {
 };
 
 constexpr int kMTileRows = 16;  // positions per tile
-constexpr int kMWaves = kMWavesHost;
+// Waves per workgroup.  bf16 / fp16 caches: 4 (each wave streams twice the
+// rows and the final merge halves: config 3 77.7 vs 79.1 us at 8).  Q8_0
+// caches: 8, two waves per SIMD hiding each other's widening and LDS
+// latency (52 vs 58 us at 4).
+template <typename T>
+constexpr int mdecode_waves() {
+    return __is_same(T, q8_0_t) ? kMWavesQ8Host : kMWaves16Host;
+}
 // Tiles of K and V in flight per wave.  With the tile loop's exact waits, 2
 // beats 3 (3 spills registers for Q8_0 and fp16 caches, and was 0.5% slower
 // for bf16 at config 3).
@@ -2527,7 +2534,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     constexpr int ROWB = KV * kHeadDim * 2;                // bytes per row of the 16-bit LDS V tile
     constexpr int CPR = ROWB / 16, NKB = 2 * KV, NMB = 4 * KV;
     constexpr int NH = KV * G;
-    constexpr int NW = kMWaves, D = kMDepth;
+    constexpr int NW = mdecode_waves<T>(), D = kMDepth;
     constexpr bool PAGED = is_paged(MODE);
     constexpr bool LAYER = is_layer(MODE);
     static_assert(NH <= 16, "query heads are the 16 MFMA columns");
@@ -2915,7 +2922,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
 template <typename T, int G, int KV, int MODE>
 __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     constexpr int NH = KV * G;
-    constexpr int NW = kMWaves;
+    constexpr int NW = mdecode_waves<T>();
     constexpr bool PAGED = is_paged(MODE);
     constexpr bool LAYER = is_layer(MODE);
     int split = blockIdx.x, seq = blockIdx.y;
@@ -2964,7 +2971,7 @@ __device__ __forceinline__ void mdecode_sk_body(const DecodeArgs& a) {
     constexpr int NH = KV * G;
     int64_t S, lo, hi, P;
     int last_u, s, len = 0;
-    if (!sk_locate<kMWaves * 64, false>(a, S, lo, hi, last_u, s, P)) return;
+    if (!sk_locate<mdecode_waves<T>() * 64, false>(a, S, lo, hi, last_u, s, P)) return;
     for (bool first = true; sk_seek<false>(a, lo, hi, s, P, len); ++s, first = false) {
         if (!first) __syncthreads();  // the previous segment's merge reads the LDS this one's tiles reuse
         const int64_t r0 = max(lo - P, (int64_t)0), r1 = min(hi - P, (int64_t)len);
@@ -2978,31 +2985,31 @@ __device__ __forceinline__ void mdecode_sk_body(const DecodeArgs& a) {
 }
 
 #define TMAC_MDECODE_KERNELS_T(G, KV, TN, T)                                                          \
-    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_u_##TN##_g##G##_kv##KV(     \
+    extern "C" __global__ __launch_bounds__(mdecode_waves<T>() * 64) void tmac_mdecode_u_##TN##_g##G##_kv##KV(     \
         DecodeArgs a) {                                                                                \
         mdecode_body<T, G, KV, kUniform>(a);                                                           \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_r_##TN##_g##G##_kv##KV(     \
+    extern "C" __global__ __launch_bounds__(mdecode_waves<T>() * 64) void tmac_mdecode_r_##TN##_g##G##_kv##KV(     \
         DecodeArgs a) {                                                                                \
         mdecode_body<T, G, KV, kRagged>(a);                                                            \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_p_##TN##_g##G##_kv##KV(     \
+    extern "C" __global__ __launch_bounds__(mdecode_waves<T>() * 64) void tmac_mdecode_p_##TN##_g##G##_kv##KV(     \
         DecodeArgs a) {                                                                                \
         mdecode_body<T, G, KV, kPaged>(a);                                                             \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_l_##TN##_g##G##_kv##KV(     \
+    extern "C" __global__ __launch_bounds__(mdecode_waves<T>() * 64) void tmac_mdecode_l_##TN##_g##G##_kv##KV(     \
         DecodeArgs a) {                                                                                \
         mdecode_body<T, G, KV, kLayer>(a);                                                             \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_pl_##TN##_g##G##_kv##KV(    \
+    extern "C" __global__ __launch_bounds__(mdecode_waves<T>() * 64) void tmac_mdecode_pl_##TN##_g##G##_kv##KV(    \
         DecodeArgs a) {                                                                                \
         mdecode_body<T, G, KV, kPagedLayer>(a);                                                        \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_sk_##TN##_g##G##_kv##KV(    \
+    extern "C" __global__ __launch_bounds__(mdecode_waves<T>() * 64) void tmac_mdecode_sk_##TN##_g##G##_kv##KV(    \
         DecodeArgs a) {                                                                                \
         mdecode_sk_body<T, G, KV, false>(a);                                                           \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(kMWaves * 64) void tmac_mdecode_sk_p_##TN##_g##G##_kv##KV(  \
+    extern "C" __global__ __launch_bounds__(mdecode_waves<T>() * 64) void tmac_mdecode_sk_p_##TN##_g##G##_kv##KV(  \
         DecodeArgs a) {                                                                                \
         mdecode_sk_body<T, G, KV, true>(a);                                                            \
     }

@@ -275,7 +275,7 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
             auto f = tab.find({g, n_kv_head});
             if (f != tab.end()) {
                 k->group = f->second;
-                k->group_waves = tmac::kMWavesHost;
+                k->group_waves = dt == TMAC_KV_Q8_0 ? tmac::kMWavesQ8Host : tmac::kMWaves16Host;
             }
         }
     }
@@ -582,7 +582,7 @@ hipFunction_t stream_k_kernel(const tmac_context* ctx, int dt, bool paged, int n
     const auto& tab = ctx->mdecode_sk[dt - 1][paged ? 1 : 0];
     const auto it = tab.find(key);
     if (it == tab.end()) return nullptr;
-    *threads = tmac::kMWavesHost * 64;
+    *threads = (dt == TMAC_KV_Q8_0 ? tmac::kMWavesQ8Host : tmac::kMWaves16Host) * 64;
     return it->second;
 }
 
