@@ -70,6 +70,43 @@ __device__ __forceinline__ float slot_sum(float x) {
     return x;
 }
 
+// Max over the 8 lanes of a slot; every lane receives the same value.
+__device__ __forceinline__ float slot_max(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));
+    x = fmaxf(x, dpp<0x4E>(x));
+    return fmaxf(x, dpp<0x141>(x));
+}
+
+// Sum / max over the lanes lane ^ m, m = FIRST, 2 FIRST, ..., 32, without the
+// LDS crossbar: DPP inside 16-lane rows (FIRST = 1: the slot patterns above,
+// then lane ^ 8 = row_ror:8), then the gfx950 row swaps for lane ^ 16 and
+// lane ^ 32 (each returns both swapped registers; the pair's sum or max is the
+// same whichever way round they come).  Every lane ends with the same bits.
+template <int FIRST>
+__device__ __forceinline__ float xor_sum(float x) {
+    static_assert(FIRST == 1 || FIRST == 8 || FIRST == 16 || FIRST == 32, "lane groups of 1, 8, 16 or 32");
+    if constexpr (FIRST == 1) x = slot_sum(x);
+    if constexpr (FIRST <= 8) x += dpp<0x128>(x);
+    if constexpr (FIRST <= 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    }
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+template <int FIRST>
+__device__ __forceinline__ float xor_max(float x) {
+    static_assert(FIRST == 1 || FIRST == 8 || FIRST == 16 || FIRST == 32, "lane groups of 1, 8, 16 or 32");
+    if constexpr (FIRST == 1) x = slot_max(x);
+    if constexpr (FIRST <= 8) x = fmaxf(x, dpp<0x128>(x));
+    if constexpr (FIRST <= 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    }
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Rotation of one adjacent pair, exactly as tmac_gguf.cpp:999-1001 rounds it:
@@ -290,11 +327,8 @@ __device__ __forceinline__ void put_row<q8_0_t>(float (&x)[8], char* p, int c, b
         a0 = fmaxf(a0, fabsf(x[t]));
         a1 = fmaxf(a1, fabsf(x[4 + t]));
     }
-#pragma unroll
-    for (int mask = 1; mask < kLanesPerSlot; mask <<= 1) {
-        a0 = fmaxf(a0, __shfl_xor(a0, mask));
-        a1 = fmaxf(a1, __shfl_xor(a1, mask));
-    }
+    a0 = slot_max(a0);
+    a1 = slot_max(a1);
     unsigned d0, d1;
     const unsigned lo = quant4(x, a0, d0);
     const unsigned hi = quant4(x + 4, a1, d1);
@@ -378,9 +412,7 @@ __device__ __forceinline__ void attend(const float (&q)[G][kDimsPerLane], State<
         // Raise the wave's shared max to this step's max (rare after the first step).
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            float mx = s[g];
-#pragma unroll
-            for (int mask = kLanesPerSlot * KV; mask < 64; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
+            const float mx = xor_max<kLanesPerSlot * KV>(s[g]);
             const float mn = fmaxf(st.m[g], mx);
             const float alpha = (st.m[g] == kNegInf) ? 0.f : fast_exp2(st.m[g] - mn);
             st.l[g] *= alpha;
@@ -536,13 +568,10 @@ __device__ __forceinline__ void finish(State<G>& st, int lane, int wave, bool di
     constexpr int NH = KVS * G;
     // 1. Sum the slots of each kv group inside the wave (they share the max).
 #pragma unroll
-    for (int mask = kLanesPerSlot * KVS; mask < 64; mask <<= 1) {
+    for (int g = 0; g < G; ++g) {
+        st.l[g] = xor_sum<kLanesPerSlot * KVS>(st.l[g]);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            st.l[g] += __shfl_xor(st.l[g], mask);
-#pragma unroll
-            for (int t = 0; t < kDimsPerLane; ++t) st.acc[g][t] += __shfl_xor(st.acc[g][t], mask);
-        }
+        for (int t = 0; t < kDimsPerLane; ++t) st.acc[g][t] = xor_sum<kLanesPerSlot * KVS>(st.acc[g][t]);
     }
     // 2. Waves -> LDS.
     __shared__ float s_acc[NW][NH][kHeadDim];
@@ -1343,9 +1372,7 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
         sc = slot_sum(sc);
         sc = valid ? sc : kNegInf;
         if (__any(sc - m > kTau)) {  // raise the wave's shared max (rare after the first step)
-            float mx = sc;
-#pragma unroll
-            for (int mask = kLanesPerSlot; mask < 64; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask));
+            const float mx = xor_max<kLanesPerSlot>(sc);
             const float mn = fmaxf(m, mx);
             const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
             l *= alpha;
@@ -1379,12 +1406,9 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
     }
 
     // 6. slots -> wave total (same max), then waves through LDS
+    l = xor_sum<kLanesPerSlot>(l);
 #pragma unroll
-    for (int mask = kLanesPerSlot; mask < 64; mask <<= 1) {
-        l += __shfl_xor(l, mask);
-#pragma unroll
-        for (int t = 0; t < DV; ++t) acc[t] += __shfl_xor(acc[t], mask);
-    }
+    for (int t = 0; t < DV; ++t) acc[t] = xor_sum<kLanesPerSlot>(acc[t]);
     __shared__ float s_acc[NW][kLanesPerSlot][DV];
     __shared__ float s_ml[NW][2];
     if (slot == 0) {
@@ -1435,15 +1459,11 @@ __device__ __forceinline__ float merge_splits(const float* __restrict__ ws, int 
 #pragma unroll
         for (int j = 0; j < B; ++j) aj[j] = ws[(size_t)(c0 + min(j, n - 1)) * SP + d];
         const float mo = d < n ? ml : kNegInf;
-        float cm = mo;
-#pragma unroll
-        for (int mask = 1; mask < 64; mask <<= 1) cm = fmaxf(cm, __shfl_xor(cm, mask));
+        const float cm = xor_max<1>(mo);
         const float nm = fmaxf(M, cm);  // finite: a sequence with rows has a finite score
         const float sc = (M == kNegInf) ? 0.f : fast_exp2(M - nm);
         const float w = (mo == kNegInf) ? 0.f : fast_exp2(mo - nm);
-        float lw = d < n ? ll * w : 0.f;
-#pragma unroll
-        for (int mask = 1; mask < 64; mask <<= 1) lw += __shfl_xor(lw, mask);
+        const float lw = xor_sum<1>(d < n ? ll * w : 0.f);
         float acc = A * sc;
 #pragma unroll
         for (int j = 0; j < B; ++j) {
