@@ -426,12 +426,32 @@ def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
         ctx.prefill(dq, dk, dv, dout, n_seq, n_q, prefix, cap, NH, NKV, HD, stream=stream)
 
     per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
-    for d in (dq, dk, dv, dout):
+    # The chunked flow over the persistent tile copy: the prefix rows were packed
+    # by the earlier chunks (once, before timing); each timed call packs this
+    # chunk's 512 rows and runs the attention over the tiles.
+    tiles = ctx.empty(ctx.prefill_tiles_bytes(n_seq, NKV, cap), np.uint8)
+    ctx.prefill_pack_rows(dk, dv, cap, tiles, cap, n_seq, NKV, HD, 0, prefix, stream=stream)
+    dout2 = ctx.empty((n_seq, n_q, NH * HD))
+
+    def chunk():
+        ctx.prefill_pack_rows(dk, dv, cap, tiles, cap, n_seq, NKV, HD, prefix, cap, stream=stream)
+        ctx.prefill_tiles(dq, tiles, cap, dout2, n_seq, n_q, prefix, NH, NKV, HD, stream=stream)
+
+    per_c, mean_c = time_launches(ctx, stream, chunk, steps, warmup)
+    same = bool(np.array_equal(dout.numpy().view(np.uint32), dout2.numpy().view(np.uint32)))
+    for d in (dq, dk, dv, dout, dout2, tiles):
         d.free()
-    tflops = C5_FLOPS / (mean_ms * 1e-3) / 1e12
-    return {"mean_us": mean_ms * 1e3, "median_us": float(np.median(per)) * 1e3, "flops": C5_FLOPS,
+    tflops = C5_FLOPS / (mean_c * 1e-3) / 1e12
+    tflops_full = C5_FLOPS / (mean_ms * 1e-3) / 1e12
+    return {"mean_us": mean_c * 1e3, "median_us": float(np.median(per_c)) * 1e3, "flops": C5_FLOPS,
             "tflops": tflops, "mfma_util": tflops / MFMA_BF16_PEAK_TFLOPS,
-            "bytes": n_seq * n_q * NH * HD * 4 * 2 + n_seq * cap * KVD * 4 * 2}
+            "repack_all_mean_us": mean_ms * 1e3, "repack_all_median_us": float(np.median(per)) * 1e3,
+            "repack_all_mfma_util": tflops_full / MFMA_BF16_PEAK_TFLOPS,
+            "chunk_equals_repack_all": same,
+            "bytes": n_seq * n_q * NH * HD * 4 * 2 + n_seq * cap * KVD * 4 * 2,
+            "note": "mean_us / mfma_util: one chunk of the chunked flow (pack the chunk's 512 rows into the "
+                    "persistent bf16 tile copy, attention over the tiles; the 1536 prefix rows packed by the "
+                    "earlier chunks); repack_all_*: tmac_attention_prefill, which packs all 2048 rows per call"}
 
 
 def _cpu_facts():
@@ -630,8 +650,10 @@ def main():
             f"{extra['qkv']['stream_us_per_layer']:.2f} us/layer streaming = {extra['qkv']['stream_gbs']:.0f} GB/s")
     if "c5" in sections:
         extra["c5"] = bench_c5(ctx, stream, max(10, args.steps // 2), args.warmup)
-        log(f"[bench] C5 {extra['c5']['mean_us']:.1f} us, {extra['c5']['tflops']:.1f} TFLOP/s, "
-            f"MFMA util {extra['c5']['mfma_util'] * 100:.2f}%")
+        c5 = extra["c5"]
+        log(f"[bench] C5 chunk {c5['mean_us']:.1f} us, {c5['tflops']:.1f} TFLOP/s, MFMA util "
+            f"{c5['mfma_util'] * 100:.2f}%; repack-all call {c5['repack_all_mean_us']:.1f} us "
+            f"({c5['repack_all_mfma_util'] * 100:.2f}%); equal outputs: {c5['chunk_equals_repack_all']}")
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

@@ -344,6 +344,29 @@ int tmac_attention_prefill_paged(tmac_context* ctx, tmac_stream stream, int kv_d
                                  int max_pages, float* out, int n_seq, int n_q, int prefix_len, int n_head,
                                  int n_kv_head, int head_dim);
 
+/* Chunked prefill over a persistent bf16 tile copy of the cache (no counterpart in the
+ * reference, which has no chunked prefill; for callers that prefill a prompt chunk by
+ * chunk): the rows of earlier chunks are packed once, and each chunk packs only its own
+ * rows before its attention.  `tiles` is a caller buffer of tmac_prefill_tiles_bytes
+ * bytes for `capacity` rows per sequence (16 KiB per 64 rows and (sequence, kv head),
+ * rows rounded up to 256); it is valid for the rows packed so far and the caller keeps
+ * it in step with the cache (repack rows that change).
+ *   tmac_prefill_pack_rows: packs rows row_begin .. row_end - 1 of every sequence (whole
+ *     64-row tiles: rows below row_end from the cache, the rest of the last tile zero).
+ *     Cache layout and kv_dtype as tmac_attention_prefill_kv; row_end <= capacity,
+ *     seq_stride >= capacity when n_seq > 1.
+ *   tmac_attention_prefill_tiles: the attention of tmac_attention_prefill over the tiles,
+ *     which must hold rows 0 .. prefix_len + n_q - 1 (prefix_len + n_q <= capacity).
+ * pack_rows(0, prefix_len + n_q) then attention_prefill_tiles gives the outputs of
+ * tmac_attention_prefill bit for bit (the same kernels on the same tiles). */
+size_t tmac_prefill_tiles_bytes(int n_seq, int n_kv_head, int capacity);
+int tmac_prefill_pack_rows(tmac_context* ctx, tmac_stream stream, int kv_dtype, const void* k_cache,
+                           const void* v_cache, int64_t seq_stride, void* tiles, int capacity, int n_seq,
+                           int n_kv_head, int head_dim, int row_begin, int row_end);
+int tmac_attention_prefill_tiles(tmac_context* ctx, tmac_stream stream, const float* q, const void* tiles,
+                                 int capacity, float* out, int n_seq, int n_q, int prefix_len, int n_head,
+                                 int n_kv_head, int head_dim);
+
 /* ---- tuning / introspection ---- */
 enum tmac_option {
     TMAC_OPT_SPLIT_LEN = 1,     /* group kernel: rows per workgroup; 0 = automatic (default) */

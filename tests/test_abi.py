@@ -41,9 +41,22 @@ def test_calls_without_context_are_rejected():
     assert lib.tmac_layer_attention(None, None, 16, 16, 16, 16, 16, 16, 14, 2, 64, 0, 256, 1e6) == nc
     assert lib.tmac_attention_decode_batched(None, None, 16, 16, 16, 16, 1, 14, 2, 64, 1, 1) == nc
     assert lib.tmac_attention_decode_ragged(None, None, 16, 16, 16, 16, 16, 16, 1, 14, 2, 64, 1, 0) == nc
+    assert lib.tmac_prefill_pack_rows(None, None, 0, 16, 16, 16, 16, 16, 1, 2, 64, 0, 1) == nc
+    assert lib.tmac_attention_prefill_tiles(None, None, 16, 16, 16, 16, 1, 1, 0, 14, 2, 64) == nc
     assert lib.tmac_step_begin(None, None) == nc
     assert lib.tmac_malloc(None, ctypes.byref(ctypes.c_void_p()), 16) == nc
     assert lib.tmac_shutdown(None) == nc
+
+
+def test_prefill_tiles_bytes():
+    """16 KiB per 64-row tile and (sequence, kv head); rows rounded up to whole 4-tile stages."""
+    lib = tmac_attn.load_library()
+    tile = 2 * 64 * 64 * 2
+    assert lib.tmac_prefill_tiles_bytes(4, 2, 2048) == 4 * 2 * 32 * tile
+    assert lib.tmac_prefill_tiles_bytes(1, 1, 1) == 4 * tile
+    assert lib.tmac_prefill_tiles_bytes(1, 2, 257) == 2 * 8 * tile
+    assert lib.tmac_prefill_tiles_bytes(0, 2, 100) == 0
+    assert lib.tmac_prefill_tiles_bytes(1, 0, 100) == 0 and lib.tmac_prefill_tiles_bytes(1, 2, 0) == 0
 
 
 def test_init_without_gpu_fails_cleanly():

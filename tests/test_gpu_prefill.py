@@ -229,6 +229,58 @@ def test_chunked_prompt_rope_rows_write_prefill(ctx, dt):
     assert ctx.check_device_error() == 0
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16", "q8"])
+def test_prefill_tiles_chunks_match_full_call(ctx, dt):
+    """Chunked prefill over the persistent tile copy: each chunk packs only its
+    own rows (tmac_prefill_pack_rows, chunk starts not on 64-row tiles) and
+    attends through tmac_attention_prefill_tiles.  Every chunk's outputs equal
+    tmac_attention_prefill's on the same cache bit for bit, and the oracle's on
+    the bf16-rounded inputs within the fp32 tolerance."""
+    import tmac_attn
+    n_seq, nh, nkv, cap = 2, 14, 2, 700
+    q, k, v = (bf16_round(a) for a in make(970, n_seq, cap, 0, cap, nh, nkv))
+    code = {"f32": tmac_attn.TMAC_KV_F32, "bf16": tmac_attn.TMAC_KV_BF16, "q8": tmac_attn.TMAC_KV_Q8_0}[dt]
+    if dt == "f32":
+        kb, vb, kw, vw = k, v, k, v
+    elif dt == "bf16":  # bf16-exact values: the cache holds them exactly
+        kb, vb = ((x.view(np.uint32) >> 16).astype(np.uint16) for x in (k, v))
+        kw, vw = k, v
+    else:
+        kb, vb = (oracle.q8_kv_rows(x.reshape(-1, HD)).reshape(n_seq, cap, nkv * oracle.Q8_HEAD_BYTES) for x in (k, v))
+        kw, vw = (bf16_round(oracle.q8_kv_widen(b).reshape(n_seq, cap, nkv * HD)) for b in (kb, vb))
+    dk, dv = ctx.upload(kb), ctx.upload(vb)
+    tiles = ctx.empty(ctx.prefill_tiles_bytes(n_seq, nkv, cap), np.uint8)
+    for c0, c1 in ((0, 200), (200, 450), (450, 700)):
+        n = c1 - c0
+        dq = ctx.upload(np.ascontiguousarray(q[:, c0:c1]))
+        ctx.prefill_pack_rows(dk, dv, cap, tiles, cap, n_seq, nkv, HD, c0, c1, kv_dtype=code)
+        out_t, out_f = ctx.empty((n_seq, n, nh * HD)), ctx.empty((n_seq, n, nh * HD))
+        ctx.prefill_tiles(dq, tiles, cap, out_t, n_seq, n, c0, nh, nkv, HD)
+        ctx.prefill(dq, dk, dv, out_f, n_seq, n, c0, cap, nh, nkv, HD, kv_dtype=code)
+        got = out_t.numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), out_f.numpy().view(np.uint32), err_msg=f"chunk {c0} {dt}")
+        ref = oracle.prefill(np.ascontiguousarray(q[:, c0:c1]), kw, vw, n_seq, n, c0, cap, nh, nkv, HD, n_threads=8)
+        assert_close(got, ref, f"chunk {c0} ({dt}) vs oracle")
+    assert ctx.check_device_error() == 0
+
+
+def test_prefill_tiles_rejects_bad_arguments(ctx):
+    import tmac_attn
+    d = ctx.empty(4096)
+    cap = 100
+    tiles = ctx.empty(ctx.prefill_tiles_bytes(2, 2, cap), np.uint8)
+    bad = tmac_attn.TMAC_ERR_INVALID_ARG
+    assert ctx.prefill_pack_rows(d, d, cap, tiles, cap, 2, 2, HD, 0, cap + 1, check=False) == bad  # past capacity
+    assert ctx.prefill_pack_rows(d, d, cap, tiles, cap, 2, 2, HD, 10, 5, check=False) == bad  # end before begin
+    assert ctx.prefill_pack_rows(d, d, cap - 1, tiles, cap, 2, 2, HD, 0, 10, check=False) == bad  # stride < capacity
+    assert ctx.prefill_pack_rows(d, d, cap, tiles, cap, 2, 2, 32, 0, 10, check=False) == tmac_attn.TMAC_ERR_UNSUPPORTED
+    assert ctx.prefill_tiles(d, tiles, cap, d, 2, 60, 50, 14, 2, HD, check=False) == bad  # rows past capacity
+    assert ctx.prefill_tiles(d, tiles, cap, d, 2, 10, 0, 14, 3, HD, check=False) == bad
+    assert ctx.prefill_tiles(d, None, cap, d, 2, 10, 0, 14, 2, HD, check=False) == tmac_attn.TMAC_ERR_NULL_POINTER
+    assert ctx.prefill_tiles_bytes(2, 2, cap) == 2 * 2 * 4 * 64 * 64 * 2 * 2  # 100 rows -> 4 tiles (one stage)
+    assert ctx.check_device_error() == 0
+
+
 def test_prefill_rejects_bad_arguments(ctx):
     import tmac_attn
     d = ctx.empty(16 * 14 * HD)

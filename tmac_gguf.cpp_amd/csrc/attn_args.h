@@ -86,8 +86,10 @@ struct PrefillArgs {
     int n_qblk;              // ceil(n_q / kPrefillQueries); attention grid = n_qblk * n_kv_head * n_seq
     float qscale;            // log2(e) / sqrt(head_dim)
     uint16_t* packed;        // bf16 tiles [n_seq][n_kv_head][n_tp][K tile, V^T tile] (64 x 64 each)
-    int n_tp;                // tiles per (sequence, kv head): ceil(n_rows / 64) rounded up to a stage
-    int n_rows;              // prefix_len + n_q: cache rows that are packed
+    int n_tp;                // tiles per (sequence, kv head): ceil(rows / 64) rounded up to a stage
+    int n_rows;              // pack: rows below this are cache rows, the rest of a tile is zero
+    int tile0;               // pack: first tile of every (sequence, kv head) this launch packs
+    int n_tpp;               // pack: tiles per (sequence, kv head) this launch packs
     // paged caches: k / v are pools of n_pages kPageRows-row pages, sequence s's
     // row r in pool page block_table[s][r / kPageRows] (seq_stride unused)
     const int32_t* block_table;

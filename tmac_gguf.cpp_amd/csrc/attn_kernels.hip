@@ -1934,12 +1934,13 @@ __device__ __forceinline__ float sum4_rows(float v) {
 // threads, thread t owns row t / 4 and the 8-dim chunks q4 and 4 + q4
 // (q4 = t % 4) of the K tile and of the V^T tile.  Values are widened exactly
 // to fp32 (load_row) and rounded to bf16 (nearest even; exact for a bf16
-// cache).  Rows at or past n_rows are written as zeros.
+// cache).  Rows at or past n_rows are written as zeros.  A launch packs the
+// tiles tile0 .. tile0 + n_tpp - 1 of every (sequence, kv head).
 template <typename T, int KV, bool PAGED>
 __device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
     constexpr int HB = CacheFmt<T>::kHeadBytes, ROWB = KV * HB, DB = CacheFmt<T>::kDimBytes;
-    const int tile = blockIdx.x % a.n_tp;
-    const int rest = blockIdx.x / a.n_tp;
+    const int tile = a.tile0 + blockIdx.x % a.n_tpp;
+    const int rest = blockIdx.x / a.n_tpp;
     const int kv = rest % KV, seq = rest / KV;
     const int tid = threadIdx.x, r = tid >> 2, q4 = tid & 3;
     const int key = tile * kPrefillKeys + r;

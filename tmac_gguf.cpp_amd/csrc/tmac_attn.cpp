@@ -1192,7 +1192,7 @@ static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const flo
     const size_t pack_bytes = (size_t)pack_blocks * kPrefillTileElems * sizeof(uint16_t);
     if ((rc = ensure_workspace(ctx, (hipStream_t)stream, pack_bytes / sizeof(float)))) return rc;
     PrefillArgs a{q, static_cast<const float*>(k_cache), static_cast<const float*>(v_cache), out, seq_stride, n_q,
-                  prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(workspace(ctx)), n_tp, n_rows,
+                  prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(workspace(ctx)), n_tp, n_rows, 0, n_tp,
                   block_table, max_pages, n_pages, ctx->err};
     if ((rc = launch(ctx, ctx->prefill_pack[block_table ? 1 : 0][dt].at(n_kv_head), (unsigned)pack_blocks, 1, 256,
                      (hipStream_t)stream, &a)))
@@ -1225,6 +1225,78 @@ int tmac_attention_prefill_paged(tmac_context* ctx, tmac_stream stream, int kv_d
     }
     return prefill_impl(ctx, stream, kv_dtype, q, k_pages, v_pages, out, n_seq, n_q, prefix_len, 0, n_head,
                         n_kv_head, head_dim, block_table, max_pages, n_pages);
+}
+
+// Persistent tile copy for chunked prefill: tiles per (sequence, kv head) for
+// `capacity` cache rows, as the attention kernel strides them.
+static int prefill_tiles_per_head(int capacity) {
+    return ((capacity + kPrefillKeys - 1) / kPrefillKeys + kPrefillStageTiles - 1) / kPrefillStageTiles *
+           kPrefillStageTiles;
+}
+
+size_t tmac_prefill_tiles_bytes(int n_seq, int n_kv_head, int capacity) {
+    if (n_seq < 0 || n_kv_head < 1 || capacity < 1) return 0;
+    return (size_t)n_seq * (size_t)n_kv_head * (size_t)prefill_tiles_per_head(capacity) * kPrefillTileElems *
+           sizeof(uint16_t);
+}
+
+int tmac_prefill_pack_rows(tmac_context* ctx, tmac_stream stream, int kv_dtype, const void* k_cache,
+                           const void* v_cache, int64_t seq_stride, void* tiles, int capacity, int n_seq,
+                           int n_kv_head, int head_dim, int row_begin, int row_end) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    const int dt = kv_dtype;
+    if (dt != TMAC_KV_F32 && dt != TMAC_KV_BF16 && dt != TMAC_KV_F16 && dt != TMAC_KV_Q8_0)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_pack_rows: kv_dtype must be TMAC_KV_F32, _BF16, _F16 or _Q8_0");
+    if (!k_cache || !v_cache || !tiles) return fail(ctx, TMAC_ERR_NULL_POINTER, "prefill_pack_rows: null buffer");
+    if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(tiles))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "prefill_pack_rows: buffers must be 16-byte aligned");
+    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "prefill_pack_rows: head_dim must be 64");
+    if (ctx->prefill_pack[0][dt].find(n_kv_head) == ctx->prefill_pack[0][dt].end())
+        return fail(ctx, TMAC_ERR_UNSUPPORTED, "prefill_pack_rows: unsupported n_kv_head");
+    if (n_seq < 0 || capacity < 1 || row_begin < 0 || row_end < row_begin || row_end > capacity)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_pack_rows: need 0 <= row_begin <= row_end <= capacity");
+    if (n_seq > 1 && seq_stride < capacity)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_pack_rows: seq_stride must cover capacity rows");
+    if (n_seq == 0 || row_end == row_begin) return TMAC_OK;
+    const int n_tp = prefill_tiles_per_head(capacity);
+    const int t0 = row_begin / kPrefillKeys, t1 = (row_end + kPrefillKeys - 1) / kPrefillKeys;
+    const int64_t blocks = (int64_t)(t1 - t0) * n_kv_head * n_seq;
+    if (blocks > INT_MAX || (int64_t)n_tp * n_kv_head * n_seq > INT_MAX)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_pack_rows: too many cache tiles");
+    if ((rc = set_device(ctx))) return rc;
+    // Whole tiles t0 .. t1 - 1: rows below row_end from the cache, the rest zero.
+    PrefillArgs a{nullptr, static_cast<const float*>(k_cache), static_cast<const float*>(v_cache), nullptr,
+                  seq_stride, 0, 0, 0, kQScale, static_cast<uint16_t*>(tiles), n_tp, row_end, t0, t1 - t0,
+                  nullptr, 0, 0, ctx->err};
+    return launch(ctx, ctx->prefill_pack[0][dt].at(n_kv_head), (unsigned)blocks, 1, 256, (hipStream_t)stream, &a);
+}
+
+int tmac_attention_prefill_tiles(tmac_context* ctx, tmac_stream stream, const float* q, const void* tiles,
+                                 int capacity, float* out, int n_seq, int n_q, int prefix_len, int n_head,
+                                 int n_kv_head, int head_dim) {
+    int rc = check_ctx(ctx);
+    if (rc) return rc;
+    if (!q || !tiles || !out) return fail(ctx, TMAC_ERR_NULL_POINTER, "prefill_tiles: null buffer");
+    if (!aligned16(q) || !aligned16(tiles) || !aligned16(out))
+        return fail(ctx, TMAC_ERR_MISALIGNED, "prefill_tiles: buffers must be 16-byte aligned");
+    if (head_dim != kHeadDim) return fail(ctx, TMAC_ERR_UNSUPPORTED, "prefill_tiles: head_dim must be 64");
+    if ((rc = check_shape(ctx, n_head, n_kv_head, head_dim, nullptr, kModeUniform))) return rc;
+    if (n_seq < 0 || n_q < 0 || prefix_len < 0 || capacity < 1 || (int64_t)prefix_len + n_q > capacity)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_tiles: need n_seq, n_q, prefix_len >= 0 and "
+                                               "prefix_len + n_q <= capacity");
+    if ((int64_t)((n_q + kPrefillQueries - 1) / kPrefillQueries) * n_kv_head * n_seq > INT_MAX)
+        return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_tiles: too many (query block, kv head, sequence) units");
+    if (n_seq == 0 || n_q == 0) return TMAC_OK;
+    auto it = ctx->prefill.find({n_head / n_kv_head, n_kv_head});
+    if (it == ctx->prefill.end()) return fail(ctx, TMAC_ERR_UNSUPPORTED, "prefill_tiles: unsupported group");
+    if ((rc = set_device(ctx))) return rc;
+    const int n_qblk = (n_q + kPrefillQueries - 1) / kPrefillQueries;
+    PrefillArgs a{q, nullptr, nullptr, out, 0, n_q, prefix_len, n_qblk, kQScale,
+                  static_cast<uint16_t*>(const_cast<void*>(tiles)), prefill_tiles_per_head(capacity),
+                  prefix_len + n_q, 0, 0, nullptr, 0, 0, ctx->err};
+    return launch(ctx, it->second, (unsigned)((int64_t)n_qblk * n_kv_head * n_seq), 1, kPrefillWaves * 64,
+                  (hipStream_t)stream, &a);
 }
 
 int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add) {

@@ -106,6 +106,9 @@ SIGNATURES = {
     "tmac_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_attention_prefill_kv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i, _i, _i]),
     "tmac_attention_prefill_paged": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i]),
+    "tmac_prefill_tiles_bytes": (_sz, [_i, _i, _i]),
+    "tmac_prefill_pack_rows": (_i, [_vp, _vp, _i, _vp, _vp, _i64, _vp, _i, _i, _i, _i, _i, _i]),
+    "tmac_attention_prefill_tiles": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i]),
     "tmac_rope_rows": (_i, [_vp, _vp, _vp, _i, _i64, _i, _i, _i, _f]),
     "tmac_set_option": (_i, [_vp, _i, _i64]),
     "tmac_query_split": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
@@ -538,6 +541,25 @@ class Context:
                                                     n_seq, n_q, prefix_len, seq_stride, n_head, n_kv_head, head_dim)
         if check:
             self._check(rc, "prefill")
+        return rc
+
+    def prefill_tiles_bytes(self, n_seq, n_kv_head, capacity) -> int:
+        return int(self.lib.tmac_prefill_tiles_bytes(n_seq, n_kv_head, capacity))
+
+    def prefill_pack_rows(self, k, v, seq_stride, tiles, capacity, n_seq, n_kv_head, head_dim, row_begin, row_end,
+                          stream=None, check=True, kv_dtype=TMAC_KV_F32) -> int:
+        rc = self.lib.tmac_prefill_pack_rows(self.handle, stream, kv_dtype, _p(k), _p(v), seq_stride, _p(tiles),
+                                             capacity, n_seq, n_kv_head, head_dim, row_begin, row_end)
+        if check:
+            self._check(rc, "prefill_pack_rows")
+        return rc
+
+    def prefill_tiles(self, q, tiles, capacity, out, n_seq, n_q, prefix_len, n_head, n_kv_head, head_dim,
+                      stream=None, check=True) -> int:
+        rc = self.lib.tmac_attention_prefill_tiles(self.handle, stream, _p(q), _p(tiles), capacity, _p(out), n_seq,
+                                                   n_q, prefix_len, n_head, n_kv_head, head_dim)
+        if check:
+            self._check(rc, "prefill_tiles")
         return rc
 
     def prefill_paged(self, q, k_pages, v_pages, n_pages, block_table, max_pages, out, n_seq, n_q, prefix_len,
