@@ -255,3 +255,31 @@ def test_decode_mfma_shapes(ctx, dt, g, kv):
                                   kv, HD, n_threads=8)
     assert_close(dout.numpy()[:2], ref, f"batched dt={dt} g={g} kv={kv}")
     assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("dt", [tmac_attn.TMAC_KV_BF16, tmac_attn.TMAC_KV_F16, tmac_attn.TMAC_KV_Q8_0])
+@pytest.mark.parametrize("kscale,qscale", [(8.0, 1.0), (1.0, 8.0), (8.0, 0.125), (0.01, 30.0)])
+def test_mfma_query_parts_precision(ctx, dt, kscale, qscale):
+    """The MFMA decode's query split: three bf16 parts for a bf16 cache (fp32
+    exactly), two fp16 parts for fp16 and Q8_0 caches (representation error
+    <= 2^-22 |q|).  Keys 8x larger than the query, and the reverse, with
+    scores up to a few hundred in log2 units where the lazy max and the exp2
+    are most sensitive: still within the fp32 contract on every output."""
+    n_seq, n_pos = 4, 2048
+    q = oracle.normal(1700, (n_seq, NH * HD)) * np.float32(qscale)
+    k = oracle.normal(1701, (n_seq * n_pos, KVD)) * np.float32(kscale)
+    v = oracle.normal(1702, (n_seq * n_pos, KVD))
+    if dt == tmac_attn.TMAC_KV_Q8_0:
+        kb = oracle.q8_kv_rows(k.reshape(-1, HD)).reshape(n_seq * n_pos, -1)
+        vb = oracle.q8_kv_rows(v.reshape(-1, HD)).reshape(n_seq * n_pos, -1)
+        kw = oracle.q8_kv_widen(kb).reshape(-1, KVD)
+        vw = oracle.q8_kv_widen(vb).reshape(-1, KVD)
+    else:
+        kb, vb = to16(k, dt), to16(v, dt)
+        kw, vw = widen(kb, dt).reshape(-1, KVD), widen(vb, dt).reshape(-1, KVD)
+    dq, dk, dv, dout = ctx.upload(q), ctx.upload(kb), ctx.upload(vb), ctx.empty((n_seq, NH * HD))
+    ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, kv_dtype=dt)
+    offs = np.arange(n_seq, dtype=np.int64) * n_pos
+    ref = oracle.attention_ragged(q, kw, vw, offs, np.full(n_seq, n_pos, np.int32), NH, NKV, HD, n_threads=8)
+    assert_close(dout.numpy(), ref, f"dt={dt} keys x{kscale} query x{qscale}")
+    assert ctx.check_device_error() == 0
