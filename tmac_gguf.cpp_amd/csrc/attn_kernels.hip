@@ -1444,35 +1444,57 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
 // and the l-weighted sum are wave reductions, and split j's weight reaches
 // every lane by readlane, so a chunk costs one memory latency; later chunks
 // (more than 32 splits) rescale by the running max.
-// Merged value of output dim d over n_act partials, the first at ws (the
-// head's partial in that slot) and the rest SP floats apart.
+// One chunk of up to 32 partials: lane d's (m, l) of split c0 + d and its dim d
+// of every acc vector of the chunk, splits at or past `bound` clamped to the
+// last one below it (in bounds; masked by the merge).
+constexpr int kMergeChunk = 32;
+struct MergeChunk {
+    float ml, ll, aj[kMergeChunk];
+};
 template <int SP>
-__device__ __forceinline__ float merge_splits(const float* __restrict__ ws, int n_act, int d) {
-    constexpr int B = 32;
+__device__ __forceinline__ MergeChunk load_chunk(const float* __restrict__ ws, int c0, int bound, int d) {
+    MergeChunk ch;
+    const int sl = min(c0 + d, bound - 1);
+    ch.ml = ws[(size_t)sl * SP + kHeadDim];
+    ch.ll = ws[(size_t)sl * SP + kHeadDim + 1];
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) ch.aj[j] = ws[(size_t)min(c0 + j, bound - 1) * SP + d];
+    return ch;
+}
+// Folds the first n splits of a chunk into the running (M, L, A).  Only splits
+// j < n enter (a select, so that stale slots past n never reach the sums).
+__device__ __forceinline__ void merge_chunk(const MergeChunk& ch, int n, int d, float& M, float& L, float& A) {
+    const float mo = d < n ? ch.ml : kNegInf;
+    const float cm = xor_max<1>(mo);
+    const float nm = fmaxf(M, cm);  // finite: a sequence with rows has a finite score
+    const float sc = (M == kNegInf) ? 0.f : fast_exp2(M - nm);
+    const float w = (mo == kNegInf) ? 0.f : fast_exp2(mo - nm);
+    const float lw = xor_sum<1>(d < n ? ch.ll * w : 0.f);
+    float acc = A * sc;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+        acc = j < n ? fmaf(ch.aj[j], wj, acc) : acc;
+    }
+    A = acc;
+    L = fmaf(L, sc, lw);
+    M = nm;
+}
+// Merged value of output dim d over n_act partials, the first at ws (the
+// head's partial in that slot) and the rest SP floats apart; `first` is the
+// first chunk when the caller loaded it already.
+template <int SP>
+__device__ __forceinline__ float merge_splits(const float* __restrict__ ws, int n_act, int d,
+                                              const MergeChunk* first = nullptr) {
     float M = kNegInf, L = 0.f, A = 0.f;
-    for (int c0 = 0; c0 < n_act; c0 += B) {
-        const int n = min(B, n_act - c0);
-        const int sl = c0 + min(d, n - 1);
-        const float ml = ws[(size_t)sl * SP + kHeadDim];
-        const float ll = ws[(size_t)sl * SP + kHeadDim + 1];
-        float aj[B];
-#pragma unroll
-        for (int j = 0; j < B; ++j) aj[j] = ws[(size_t)(c0 + min(j, n - 1)) * SP + d];
-        const float mo = d < n ? ml : kNegInf;
-        const float cm = xor_max<1>(mo);
-        const float nm = fmaxf(M, cm);  // finite: a sequence with rows has a finite score
-        const float sc = (M == kNegInf) ? 0.f : fast_exp2(M - nm);
-        const float w = (mo == kNegInf) ? 0.f : fast_exp2(mo - nm);
-        const float lw = xor_sum<1>(d < n ? ll * w : 0.f);
-        float acc = A * sc;
-#pragma unroll
-        for (int j = 0; j < B; ++j) {
-            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
-            acc = fmaf(aj[j], j < n ? wj : 0.f, acc);
+    for (int c0 = 0; c0 < n_act; c0 += kMergeChunk) {
+        const int n = min(kMergeChunk, n_act - c0);
+        if (c0 == 0 && first) {
+            merge_chunk(*first, n, d, M, L, A);
+        } else {
+            const MergeChunk ch = load_chunk<SP>(ws, c0, n_act, d);
+            merge_chunk(ch, n, d, M, L, A);
         }
-        A = acc;
-        L = fmaf(L, sc, lw);
-        M = nm;
     }
     return A / L;
 }
@@ -1482,14 +1504,18 @@ __device__ __forceinline__ void combine_body(const DecodeArgs& a) {
     constexpr int NH = KV * G;
     constexpr int SP = NH * kPartialStride;  // floats between splits
     const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+    // The first chunk's loads go out with the length read: the sequence's
+    // n_splits slots are allocated whatever its length (stale slots past its
+    // active splits are masked), so one memory latency instead of two.
+    const float* ws = a.ws + (size_t)seq * a.n_splits * SP + (size_t)h * kPartialStride;
+    const MergeChunk first = load_chunk<SP>(ws, 0, a.n_splits, d);
     int n_pos, pos;
     size_t base;
     if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) return;
     if (n_pos <= 0) return;
     const int n_act = (n_pos + a.split_len - 1) / a.split_len;
     if (n_act <= 1 || n_act > a.n_splits) return;
-    const float* ws = a.ws + (size_t)seq * a.n_splits * SP + (size_t)h * kPartialStride;
-    a.out[((size_t)seq * NH + h) * kHeadDim + d] = merge_splits<SP>(ws, n_act, d);
+    a.out[((size_t)seq * NH + h) * kHeadDim + d] = merge_splits<SP>(ws, n_act, d, &first);
 }
 
 // Combine of the stream-K ragged decode: one wave per (head, sequence).  It
