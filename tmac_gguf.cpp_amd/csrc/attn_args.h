@@ -28,6 +28,15 @@ constexpr int kAnyMaxDim = 256;     // any-shape kernel and RoPE: even head_dim 
 constexpr int kMaxSplits = 256;     // split-KV workgroups per sequence, at most
 constexpr int kPartialStride = kHeadDim + 2;  // per (split, head): acc[64], m, l
 
+// RoPE row cache of one device-side position counter: two slots, slot s =
+// 32 (cos, sin) pairs at float2 offset 32 s, and at float2 offset 64 the
+// slots' tags, int [2][4] = {position, RoPE table address low 32 bits, high
+// 32 bits, 0}.  A layer kernel at position p reads both slots while it reads
+// p, uses the one tagged (p, its table) if any, and writes row p + 1 of its
+// table into slot (p + 1) % 2 for the next step.  Tags start at -1.
+constexpr int kPosSlotBytes = 1024;
+constexpr int kPosSlotBlocks = 64;   // position counters with a row cache per context
+
 // Attention over a KV cache in the reference layout: one row per position,
 // row = [n_kv_head][64] fp32 (tmac_gguf.cpp:200-201).
 struct DecodeArgs {
@@ -54,6 +63,10 @@ struct DecodeArgs {
     float* v_out;
     const float2* rope_cs;   // [rope_rows][32] (cos, sin) of pos*theta_j
     const int* pos_dev;      // device-side position (graph replay); null -> pos_host
+    // With pos_dev: this position counter's cache of RoPE rows (kPosSlotBytes,
+    // layout below), so the row of the step's position can be read without
+    // waiting for the position; null -> the row is read after the position.
+    float2* pos_slots;
     int pos_host;
     int rope_rows;
     int capacity;            // rows in the layer cache (paged layer mode: max_pages * kPageRows)

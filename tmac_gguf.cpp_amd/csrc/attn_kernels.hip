@@ -372,6 +372,81 @@ __device__ __forceinline__ void rope8(float (&x)[8], const float2* __restrict__ 
     rotate_pair(x[6], x[7], t1.z, t1.w);
 }
 
+// RoPE row of a layer step through the position counter's row cache
+// (DecodeArgs::pos_slots): both slots are read together with the position,
+// and the row is read from the table only when neither slot is tagged with
+// (position, table), so the q / k rotation need not wait for the position.
+struct RopePrefetch {
+    float4 a0, b0, a1, b1;          // lane c's pairs 2c, 2c+1 and 16+2c, 16+2c+1 of slots 0 and 1
+    int tag0, lo0, hi0, tag1, lo1, hi1;
+};
+__device__ __forceinline__ RopePrefetch rope_prefetch(const DecodeArgs& a, int c) {
+    RopePrefetch p;
+    p.a0 = p.b0 = p.a1 = p.b1 = make_float4(0.f, 0.f, 0.f, 0.f);
+    p.tag0 = p.tag1 = -1;
+    p.lo0 = p.hi0 = p.lo1 = p.hi1 = 0;
+    if (a.pos_slots) {
+        const float2* s = a.pos_slots;
+        p.a0 = *reinterpret_cast<const float4*>(s + 2 * c);
+        p.b0 = *reinterpret_cast<const float4*>(s + 16 + 2 * c);
+        p.a1 = *reinterpret_cast<const float4*>(s + 32 + 2 * c);
+        p.b1 = *reinterpret_cast<const float4*>(s + 48 + 2 * c);
+        const int* tag = reinterpret_cast<const int*>(s + 64);
+        p.tag0 = tag[0]; p.lo0 = tag[1]; p.hi0 = tag[2];
+        p.tag1 = tag[4]; p.lo1 = tag[5]; p.hi1 = tag[6];
+    }
+    return p;
+}
+__device__ __forceinline__ void rope_pairs(const DecodeArgs& a, const RopePrefetch& p, int pos, int c, float4& t0,
+                                           float4& t1) {
+    const uint64_t tab = reinterpret_cast<uint64_t>(a.rope_cs);
+    const int lo = (int)(uint32_t)tab, hi = (int)(uint32_t)(tab >> 32);
+    const bool h0 = p.tag0 == pos && p.lo0 == lo && p.hi0 == hi;
+    const bool h1 = p.tag1 == pos && p.lo1 == lo && p.hi1 == hi;
+    if (h0 || h1) {
+        t0.x = h0 ? p.a0.x : p.a1.x; t0.y = h0 ? p.a0.y : p.a1.y;
+        t0.z = h0 ? p.a0.z : p.a1.z; t0.w = h0 ? p.a0.w : p.a1.w;
+        t1.x = h0 ? p.b0.x : p.b1.x; t1.y = h0 ? p.b0.y : p.b1.y;
+        t1.z = h0 ? p.b0.z : p.b1.z; t1.w = h0 ? p.b0.w : p.b1.w;
+    } else {
+        const float2* row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
+        t0 = *reinterpret_cast<const float4*>(row + 2 * c);
+        t1 = *reinterpret_cast<const float4*>(row + 16 + 2 * c);
+        // (waited for here, so that after the branch the compiler waits for
+        // the slot loads alone, not for every load issued since them)
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+}
+// rope8 with the lane's pairs already loaded
+__device__ __forceinline__ void rope8p(float (&x)[8], const float4& t0, const float4& t1) {
+    rotate_pair(x[0], x[1], t0.x, t0.y);
+    rotate_pair(x[2], x[3], t0.z, t0.w);
+    rotate_pair(x[4], x[5], t1.x, t1.y);
+    rotate_pair(x[6], x[7], t1.z, t1.w);
+}
+// Next step's row: threads 0..15 of one workgroup read row pos + 1 (issue
+// early) and write it, tagged, into slot (pos + 1) % 2 (at the end of the
+// kernel; the layer kernels of the next step read it).
+__device__ __forceinline__ bool rope_publisher(const DecodeArgs& a, int pos, bool first_group) {
+    return a.pos_slots && first_group && threadIdx.x < 16 && pos + 1 < a.rope_rows;
+}
+// (every lane loads, from a clamped row, so that the load needs no branch)
+__device__ __forceinline__ float4 rope_publish_load(const DecodeArgs& a, int pos) {
+    const int row = min(pos + 1, a.rope_rows - 1);
+    return *reinterpret_cast<const float4*>(a.rope_cs + (size_t)row * (kHeadDim / 2) + 2 * (threadIdx.x & 15));
+}
+__device__ __forceinline__ void rope_publish_store(const DecodeArgs& a, int pos, const float4& v) {
+    const int sl = (pos + 1) & 1;
+    *reinterpret_cast<float4*>(a.pos_slots + 32 * sl + 2 * threadIdx.x) = v;
+    if (threadIdx.x == 0) {
+        const uint64_t tab = reinterpret_cast<uint64_t>(a.rope_cs);
+        int* tag = reinterpret_cast<int*>(a.pos_slots + 64) + 4 * sl;
+        tag[0] = pos + 1;
+        tag[1] = (int)(uint32_t)tab;
+        tag[2] = (int)(uint32_t)(tab >> 32);
+    }
+}
+
 template <int G>
 struct State {
     float m[G];                // running max (log2 domain), identical across a kv group's lanes
@@ -1066,6 +1141,7 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     // 1. loads that do not depend on the length
     float q[1][kDimsPerLane];
     load8(q[0], a.q + ((size_t)seq * NH + head) * kHeadDim + 4 * c);
+    const RopePrefetch rp = rope_prefetch(a, c);  // (layer mode only: pos_slots is null otherwise)
     float kn[kDimsPerLane], vn[kDimsPerLane];
     const bool new_lane = (MODE == kLayer) && wave == 0 && slot == 0;
     if (new_lane) {
@@ -1127,10 +1203,12 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     const int mem_rows = (MODE == kLayer) ? pos : n_pos;
 
     // 3. query: RoPE (layer mode) and base-2 softmax scale
-    const float2* cs_row = nullptr;
+    const bool publisher = MODE == kLayer && rope_publisher(a, pos, blockIdx.x == 0 && blockIdx.y == 0);
+    float4 next_row, cs0, cs1;
+    if (MODE == kLayer && a.pos_slots) next_row = rope_publish_load(a, pos);
     if (MODE == kLayer) {
-        cs_row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
-        rope8(q[0], cs_row, c);
+        rope_pairs(a, rp, pos, c, cs0, cs1);
+        rope8p(q[0], cs0, cs1);
     }
 #pragma unroll
     for (int t = 0; t < kDimsPerLane; ++t) q[0][t] *= a.qscale;
@@ -1173,7 +1251,7 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     //    head writes the rotated k and v to the cache row (tmac_gguf.cpp:1090-1091).
     if (MODE == kLayer && wave == 0) {
         if (new_lane) {
-            rope8(kn, cs_row, c);
+            rope8p(kn, cs0, cs1);
             const bool store = head % G == 0;
             put_row<T>(kn, reinterpret_cast<char*>(a.k_out) + (size_t)pos * ROWB + lane_col, c, store);
             put_row<T>(vn, reinterpret_cast<char*>(a.v_out) + (size_t)pos * ROWB + lane_col, c, store);
@@ -1184,6 +1262,7 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
         attend<1, 1, true>(q, st, kn, vn, new_lane);
     }
     finish<1, 1, NW>(st, lane, wave, true, out_head, nullptr);
+    if (publisher) rope_publish_store(a, pos, next_row);
 }
 
 // Sum over all 64 lanes of a wave; every lane receives the same bits (each
@@ -1276,6 +1355,7 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
     // 1. loads that do not depend on the length
     float q[1][kDimsPerLane];
     load8(q[0], a.q + ((size_t)seq * NH + head) * kHeadDim + 4 * c);
+    const RopePrefetch rp = rope_prefetch(a, c);  // (layer mode only: pos_slots is null otherwise)
     float kn[kDimsPerLane];
     VPart<DV> vn;
     const bool new_lane = (MODE == kLayer) && wave == 0 && slot == 0;
@@ -1346,12 +1426,15 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
     }
 
     // 3. RoPE (layer mode): q, and the new row, stored now (tmac_gguf.cpp:1090-1091)
-    const float2* cs_row = nullptr;
+    const bool publisher = MODE == kLayer && rope_publisher(a, pos, blockIdx.x == 0 && blockIdx.y == 0);
+    float4 next_row;
+    if (MODE == kLayer && a.pos_slots) next_row = rope_publish_load(a, pos);
     if (MODE == kLayer) {
-        cs_row = a.rope_cs + (size_t)pos * (kHeadDim / 2);
-        rope8(q[0], cs_row, c);
+        float4 t0, t1;
+        rope_pairs(a, rp, pos, c, t0, t1);
+        rope8p(q[0], t0, t1);
         if (new_lane) {
-            rope8(kn, cs_row, c);
+            rope8p(kn, t0, t1);
             if (head % G == 0) {
                 if (vp == 0) store8(a.k_out + (size_t)pos * ROWF + kvh * kHeadDim + 4 * c, kn);
                 hv_store<VS>(a.v_out + (size_t)pos * ROWF + kvh * kHeadDim + vdim0, vn);
@@ -1435,6 +1518,7 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
         }
         out_head[hv_dim<VS>(hv_vdim0<VS>(vp, cc), t)] = A / L;
     }
+    if (publisher) rope_publish_store(a, pos, next_row);
 }
 
 // Log-sum-exp merge of the split partials: one wave per (head, sequence) with
@@ -1926,11 +2010,12 @@ __device__ __forceinline__ int vt_key(int p) {
 }
 
 // Element offset of (row, column) in a 64 x 64 bf16 tile: the 16-byte chunk
-// c / 8 of row r is stored at chunk (c / 8) ^ sw(r), sw(r) = (r ^ r / 8) % 8.
-// An MFMA operand read (16 consecutive rows, one chunk each) then touches 16
-// distinct (row parity, chunk) bank groups.
+// c / 8 of row r is stored at chunk (c / 8) ^ sw(r), sw(r) = (r' ^ r' / 8) % 8
+// with r' = r % 16.  An MFMA operand read (16 consecutive rows from a multiple
+// of 16, one chunk each) then touches 16 distinct (row parity, chunk) bank
+// groups, and the offset of row 16 b + r' is 1024 b plus that of row r'.
 __device__ __forceinline__ int tile_offset(int r, int c) {
-    const int sw = (r ^ (r >> 3)) & 7;
+    const int sw = (r ^ ((r >> 3) & 1)) & 7;
     return r * 64 + ((((c >> 3) ^ sw)) << 3) + (c & 7);
 }
 

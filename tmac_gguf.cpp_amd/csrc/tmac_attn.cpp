@@ -126,6 +126,11 @@ struct tmac_context {
     float* ws = nullptr;
     size_t ws_floats = 0;
     int* err = nullptr;
+    // RoPE row caches of the device-side position counters the layer entry
+    // points have seen (kPosSlotBlocks blocks of kPosSlotBytes, allocated and
+    // tagged empty at init); counters past the last block run without one.
+    char* pos_slot_pool = nullptr;
+    std::map<const int*, int> pos_slot_of;
     std::vector<RopeTable> rope;
     // Executable step graphs alive on this context.  A captured graph keeps
     // the workspace and RoPE-table addresses it was recorded with, so while
@@ -448,6 +453,10 @@ int rope_table(tmac_context* ctx, hipStream_t stream, int head_dim, float base, 
     HIP_TRY(ctx, hipDeviceSynchronize());
     HIP_TRY(ctx, hipMalloc(&dev, host.size() * sizeof(float2)));
     HIP_TRY(ctx, hipMemcpy(dev, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice));
+    // The position counters' RoPE row caches are tagged with table addresses;
+    // a new table may reuse a freed one's address, so every tag is cleared
+    // (the device is idle here).
+    HIP_TRY(ctx, hipMemset(ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes));
     if (found) {
         release_buffer(ctx, found->dev);
         found->dev = dev;
@@ -811,6 +820,10 @@ int tmac_init(tmac_context** out, int device) {
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
     if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
+    if ((e = hipMalloc(&ctx->pos_slot_pool, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes)) != hipSuccess)
+        return bail(hip_fail(ctx, e, "hipMalloc"));
+    if ((e = hipMemset(ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes)) != hipSuccess)
+        return bail(hip_fail(ctx, e, "hipMemset"));  // every tag -1: no slot holds a row yet
     int rc = ensure_workspace(ctx, nullptr, (size_t)1 << 20);
     if (rc) return bail(rc);
     void* scratch = nullptr;
@@ -831,6 +844,7 @@ int tmac_shutdown(tmac_context* ctx) {
         for (void* p : ctx->retired) (void)hipFree(p);
         for (tmac_graph* g : ctx->graphs) g->owner = nullptr;  // graphs destroyed later touch no context
         if (ctx->err) (void)hipFree(ctx->err);
+        if (ctx->pos_slot_pool) (void)hipFree(ctx->pos_slot_pool);
         for (auto& m : ctx->modules)
             if (m) (void)hipModuleUnload(m);
     }
@@ -963,6 +977,17 @@ int tmac_attention_decode_ragged_kv(tmac_context* ctx, tmac_stream stream, int k
                               n_kv_head, head_dim, max_len, total_rows);
 }
 
+// The RoPE row cache of a device-side position counter (one block per
+// counter, assigned on first use; null once the pool is used up).
+static float2* pos_slots_for(tmac_context* ctx, const int* pos_dev) {
+    auto it = ctx->pos_slot_of.find(pos_dev);
+    if (it == ctx->pos_slot_of.end()) {
+        if ((int)ctx->pos_slot_of.size() >= tmac::kPosSlotBlocks) return nullptr;
+        it = ctx->pos_slot_of.emplace(pos_dev, (int)ctx->pos_slot_of.size()).first;
+    }
+    return reinterpret_cast<float2*>(ctx->pos_slot_pool + (size_t)it->second * tmac::kPosSlotBytes);
+}
+
 static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, const float* k_new,
                         const float* v_new, void* k_cache, void* v_cache, float* out, int n_head,
                         int n_kv_head, int head_dim, int pos, const int* pos_dev, int capacity,
@@ -996,6 +1021,7 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
     a.rope_cs = rt->dev;
     a.rope_rows = rt->rows;
     a.pos_dev = pos_dev;
+    a.pos_slots = pos_dev ? pos_slots_for(ctx, pos_dev) : nullptr;
     a.pos_host = pos;
     a.capacity = capacity;
     a.head_dim = head_dim;
