@@ -31,9 +31,10 @@ constexpr int kPartialStride = kHeadDim + 2;  // per (split, head): acc[64], m, 
 // RoPE row cache of one device-side position counter: two slots, slot s =
 // 32 (cos, sin) pairs at float2 offset 32 s, and at float2 offset 64 the
 // slots' tags, int [2][4] = {position, RoPE table address low 32 bits, high
-// 32 bits, 0}.  A layer kernel at position p reads both slots while it reads
-// p, uses the one tagged (p, its table) if any, and writes row p + 1 of its
-// table into slot (p + 1) % 2 for the next step.  Tags start at -1.
+// 32 bits, 0}.  tmac_pos_update writes row p of the table the counter's layer
+// steps use into slot p % 2 when it sets the counter to p; a layer kernel at
+// position p reads both slots while it reads p and uses the one tagged (p,
+// its table) if any.  Tags start at -1.
 constexpr int kPosSlotBytes = 1024;
 constexpr int kPosSlotBlocks = 64;   // position counters with a row cache per context
 
@@ -175,6 +176,10 @@ struct PosArgs {
     int* pos;
     int value;
     int add;                 // 0: *pos = value; 1: *pos += value
+    // the counter's RoPE row cache and the table its layer steps use (null: none)
+    float2* slots;
+    const float2* rope_cs;
+    int rope_rows;
 };
 
 }  // namespace tmac

@@ -373,9 +373,10 @@ __device__ __forceinline__ void rope8(float (&x)[8], const float2* __restrict__ 
 }
 
 // RoPE row of a layer step through the position counter's row cache
-// (DecodeArgs::pos_slots): both slots are read together with the position,
-// and the row is read from the table only when neither slot is tagged with
-// (position, table), so the q / k rotation need not wait for the position.
+// (DecodeArgs::pos_slots, filled by tmac_pos_update): both slots are read
+// together with the position, and the row is read from the table only when
+// neither slot is tagged with (position, table), so the q / k rotation need
+// not wait for the position.
 struct RopePrefetch {
     float4 a0, b0, a1, b1;          // lane c's pairs 2c, 2c+1 and 16+2c, 16+2c+1 of slots 0 and 1
     int tag0, lo0, hi0, tag1, lo1, hi1;
@@ -424,29 +425,6 @@ __device__ __forceinline__ void rope8p(float (&x)[8], const float4& t0, const fl
     rotate_pair(x[4], x[5], t1.x, t1.y);
     rotate_pair(x[6], x[7], t1.z, t1.w);
 }
-// Next step's row: threads 0..15 of one workgroup read row pos + 1 (issue
-// early) and write it, tagged, into slot (pos + 1) % 2 (at the end of the
-// kernel; the layer kernels of the next step read it).
-__device__ __forceinline__ bool rope_publisher(const DecodeArgs& a, int pos, bool first_group) {
-    return a.pos_slots && first_group && threadIdx.x < 16 && pos + 1 < a.rope_rows;
-}
-// (every lane loads, from a clamped row, so that the load needs no branch)
-__device__ __forceinline__ float4 rope_publish_load(const DecodeArgs& a, int pos) {
-    const int row = min(pos + 1, a.rope_rows - 1);
-    return *reinterpret_cast<const float4*>(a.rope_cs + (size_t)row * (kHeadDim / 2) + 2 * (threadIdx.x & 15));
-}
-__device__ __forceinline__ void rope_publish_store(const DecodeArgs& a, int pos, const float4& v) {
-    const int sl = (pos + 1) & 1;
-    *reinterpret_cast<float4*>(a.pos_slots + 32 * sl + 2 * threadIdx.x) = v;
-    if (threadIdx.x == 0) {
-        const uint64_t tab = reinterpret_cast<uint64_t>(a.rope_cs);
-        int* tag = reinterpret_cast<int*>(a.pos_slots + 64) + 4 * sl;
-        tag[0] = pos + 1;
-        tag[1] = (int)(uint32_t)tab;
-        tag[2] = (int)(uint32_t)(tab >> 32);
-    }
-}
-
 template <int G>
 struct State {
     float m[G];                // running max (log2 domain), identical across a kv group's lanes
@@ -1203,9 +1181,7 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
     const int mem_rows = (MODE == kLayer) ? pos : n_pos;
 
     // 3. query: RoPE (layer mode) and base-2 softmax scale
-    const bool publisher = MODE == kLayer && rope_publisher(a, pos, blockIdx.x == 0 && blockIdx.y == 0);
-    float4 next_row, cs0, cs1;
-    if (MODE == kLayer && a.pos_slots) next_row = rope_publish_load(a, pos);
+    float4 cs0, cs1;
     if (MODE == kLayer) {
         rope_pairs(a, rp, pos, c, cs0, cs1);
         rope8p(q[0], cs0, cs1);
@@ -1262,7 +1238,6 @@ __device__ __forceinline__ void head_body(const DecodeArgs& a) {
         attend<1, 1, true>(q, st, kn, vn, new_lane);
     }
     finish<1, 1, NW>(st, lane, wave, true, out_head, nullptr);
-    if (publisher) rope_publish_store(a, pos, next_row);
 }
 
 // Sum over all 64 lanes of a wave; every lane receives the same bits (each
@@ -1426,9 +1401,6 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
     }
 
     // 3. RoPE (layer mode): q, and the new row, stored now (tmac_gguf.cpp:1090-1091)
-    const bool publisher = MODE == kLayer && rope_publisher(a, pos, blockIdx.x == 0 && blockIdx.y == 0);
-    float4 next_row;
-    if (MODE == kLayer && a.pos_slots) next_row = rope_publish_load(a, pos);
     if (MODE == kLayer) {
         float4 t0, t1;
         rope_pairs(a, rp, pos, c, t0, t1);
@@ -1518,7 +1490,6 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
         }
         out_head[hv_dim<VS>(hv_vdim0<VS>(vp, cc), t)] = A / L;
     }
-    if (publisher) rope_publish_store(a, pos, next_row);
 }
 
 // Log-sum-exp merge of the split partials: one wave per (head, sequence) with
@@ -3365,8 +3336,31 @@ extern "C" __global__ __launch_bounds__(256) void tmac_cvt_q8(CvtArgs a) {
 }
 
 // Device-side position for graph replays: *pos = value, or *pos += value.
+// Sets or advances a device-side position; with a row cache (a.slots), also
+// writes the RoPE row of the new position into its slot (position % 2),
+// tagged with (position, table), for the layer steps that follow.
 extern "C" __global__ __launch_bounds__(64) void tmac_pos_update(PosArgs a) {
-    if (threadIdx.x == 0) *a.pos = a.add ? *a.pos + a.value : a.value;
+    __shared__ int s_pos;
+    if (threadIdx.x == 0) {
+        const int p = a.add ? *a.pos + a.value : a.value;
+        *a.pos = p;
+        s_pos = p;
+    }
+    if (!a.slots) return;
+    __syncthreads();
+    const int p = s_pos;
+    if (p < 0 || p >= a.rope_rows) return;
+    const int sl = p & 1;
+    if (threadIdx.x < 16)
+        *reinterpret_cast<float4*>(a.slots + 32 * sl + 2 * threadIdx.x) =
+            *reinterpret_cast<const float4*>(a.rope_cs + (size_t)p * (kHeadDim / 2) + 2 * threadIdx.x);
+    if (threadIdx.x == 0) {
+        const uint64_t tab = reinterpret_cast<uint64_t>(a.rope_cs);
+        int* tag = reinterpret_cast<int*>(a.slots + 64) + 4 * sl;
+        tag[0] = p;
+        tag[1] = (int)(uint32_t)tab;
+        tag[2] = (int)(uint32_t)(tab >> 32);
+    }
 }
 
 #endif  // TMAC_IN_PART(3)

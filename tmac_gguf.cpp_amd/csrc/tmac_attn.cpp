@@ -131,6 +131,8 @@ struct tmac_context {
     // tagged empty at init); counters past the last block run without one.
     char* pos_slot_pool = nullptr;
     std::map<const int*, int> pos_slot_of;
+    // the RoPE table (device rows, row count) of each counter's latest layer step
+    std::map<const int*, std::pair<const float2*, int>> pos_table_of;
     std::vector<RopeTable> rope;
     // Executable step graphs alive on this context.  A captured graph keeps
     // the workspace and RoPE-table addresses it was recorded with, so while
@@ -458,6 +460,9 @@ int rope_table(tmac_context* ctx, hipStream_t stream, int head_dim, float base, 
     // (the device is idle here).
     HIP_TRY(ctx, hipMemset(ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes));
     if (found) {
+        // counters whose row caches tmac_pos_update refreshes from this table
+        for (auto& pt : ctx->pos_table_of)
+            if (pt.second.first == found->dev) pt.second = {dev, new_rows};
         release_buffer(ctx, found->dev);
         found->dev = dev;
         found->rows = new_rows;
@@ -1022,6 +1027,7 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
     a.rope_rows = rt->rows;
     a.pos_dev = pos_dev;
     a.pos_slots = pos_dev ? pos_slots_for(ctx, pos_dev) : nullptr;
+    if (a.pos_slots) ctx->pos_table_of[pos_dev] = {rt->dev, rt->rows};
     a.pos_host = pos;
     a.capacity = capacity;
     a.head_dim = head_dim;
@@ -1330,7 +1336,15 @@ int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int val
     if (rc) return rc;
     if (!pos_dev) return fail(ctx, TMAC_ERR_NULL_POINTER, "pos_update: null pointer");
     if ((rc = set_device(ctx))) return rc;
-    PosArgs a{pos_dev, value, add ? 1 : 0};
+    PosArgs a{pos_dev, value, add ? 1 : 0, nullptr, nullptr, 0};
+    // a counter the layer steps have used: also refresh its RoPE row cache
+    const auto t = ctx->pos_table_of.find(pos_dev);
+    const auto sl = ctx->pos_slot_of.find(pos_dev);
+    if (t != ctx->pos_table_of.end() && sl != ctx->pos_slot_of.end()) {
+        a.slots = reinterpret_cast<float2*>(ctx->pos_slot_pool + (size_t)sl->second * tmac::kPosSlotBytes);
+        a.rope_cs = t->second.first;
+        a.rope_rows = t->second.second;
+    }
     return launch(ctx, ctx->k_pos, 1, 1, 64, (hipStream_t)stream, &a);
 }
 
