@@ -171,12 +171,19 @@ int tmac_layer_attention(tmac_context* ctx, tmac_stream stream, const float* q, 
 /* Same, with the position read on the device from *pos_dev at run time, so a
  * captured step graph can be replayed for successive positions.  An
  * out-of-range *pos_dev makes the kernel skip its work and raise the device
- * error word (see tmac_check_device_error). */
+ * error word (see tmac_check_device_error).
+ * The context keeps a small RoPE row cache for each of the first 64 distinct
+ * pos_dev counters it sees: tmac_pos_update fills it with the row of the
+ * position it sets, so the step rotates q and k_new without first waiting for
+ * *pos_dev.  A position written into the counter any other way is still
+ * correct (the row is then read from the table after the position). */
 int tmac_layer_attention_devpos(tmac_context* ctx, tmac_stream stream, const float* q,
                                 const float* k_new, const float* v_new, float* k_cache,
                                 float* v_cache, float* out, int n_head, int n_kv_head, int head_dim,
                                 const int* pos_dev, int capacity, float base);
-/* *pos_dev = value (add = 0) or *pos_dev += value (add = 1), as a kernel (graph safe). */
+/* *pos_dev = value (add = 0) or *pos_dev += value (add = 1), as a kernel (graph
+ * safe); for a counter the layer steps have used, also the RoPE row of the new
+ * position into that counter's row cache (see tmac_layer_attention_devpos). */
 int tmac_pos_update(tmac_context* ctx, tmac_stream stream, int* pos_dev, int value, int add);
 
 /* Builds (or extends) the cos/sin table for (head_dim, base) to cover

@@ -2,12 +2,13 @@
 
 A fused layer step reading its position from device memory (tmac_layer_attention_devpos)
 takes the RoPE row of that position from the counter's two-slot row cache when a slot is
-tagged with (position, RoPE table), and from the table otherwise; each step writes the next
-position's row into the other slot.  These tests drive the paths a graph sweep does not:
-positions that jump (no slot matches), two counters sharing one table, one counter
-alternating between two tables (RoPE bases), and more counters than the context has row
-caches.  Every output is checked against the oracle's layer step (tmac_gguf.cpp:990-1016,
-1090-1128) and the caches bit for bit."""
+tagged with (position, RoPE table), and from the table otherwise; tmac_pos_update writes the
+row of the position it sets into the cache.  These tests drive the paths a graph sweep does
+not: positions that jump, positions copied into the counter without tmac_pos_update (no slot
+matches), two counters sharing one table, one counter alternating between two tables (RoPE
+bases), and more counters than the context has row caches.  Every output is checked
+against the oracle's layer step (tmac_gguf.cpp:990-1016, 1090-1128) and the caches bit for
+bit."""
 import numpy as np
 import pytest
 
@@ -31,14 +32,17 @@ class Seq:
         self.pos = ctx.upload(np.zeros(1, np.int32))
         self.dq, self.dkn, self.dvn, self.dout = ctx.empty(QD), ctx.empty(KVD), ctx.empty(KVD), ctx.empty(QD)
 
-    def step(self, p, base, what):
+    def step(self, p, base, what, direct=False):
         q = oracle.normal(self.seed * 1000 + p, QD)
         kn = oracle.normal(self.seed * 1000 + p + 500, KVD)
         vn = oracle.normal(self.seed * 1000 + p + 700, KVD)
         self.dq.copy_from(q)
         self.dkn.copy_from(kn)
         self.dvn.copy_from(vn)
-        self.ctx.pos_update(self.pos, p)
+        if direct:  # the counter written by a copy: its row cache is not refreshed
+            self.pos.copy_from(np.array([p], np.int32))
+        else:
+            self.ctx.pos_update(self.pos, p)
         self.ctx.layer_attention_devpos(self.dq, self.dkn, self.dvn, self.kc, self.vc, self.dout, NH, NKV, HD,
                                         self.pos, self.cap, base)
         self.ctx.synchronize(None)
@@ -55,12 +59,16 @@ class Seq:
 
 
 def test_positions_that_jump(ctx):
-    """Consecutive positions hit the slot written by the previous step; a jump
-    (forward, backward, the same position twice) finds no matching slot."""
+    """Positions set through tmac_pos_update in any order (forward, backward,
+    the same twice) find their row in the cache; positions written into the
+    counter by a plain copy find a slot tagged with an older position, and the
+    row is read from the table."""
     s = Seq(ctx, 256, 31)
     try:
         for p in (0, 1, 2, 40, 41, 7, 8, 8, 200, 255, 3):
             s.step(p, 1e6, f"position {p}")
+        for p in (9, 10, 11, 100, 4):
+            s.step(p, 1e6, f"position {p} (copied into the counter)", direct=True)
         s.check_caches()
     finally:
         s.free()
@@ -69,7 +77,7 @@ def test_positions_that_jump(ctx):
 
 def test_two_counters_share_a_table(ctx):
     """Two sequences at different positions, interleaved step by step on the
-    same RoPE table: each counter's row cache holds its own next row."""
+    same RoPE table: each counter's row cache holds its own rows."""
     a, b = Seq(ctx, 256, 41), Seq(ctx, 256, 42)
     try:
         for i in range(6):
