@@ -102,6 +102,32 @@ def test_decode_batched_q8(ctx, mfma, n_seq, n_pos, kernel):
     assert_close(dout.numpy(), ref, f"batched q8 {n_seq}x{n_pos} mfma={mfma}")
 
 
+@pytest.mark.parametrize("dt", [tmac_attn.TMAC_KV_BF16, tmac_attn.TMAC_KV_F16, Q8])
+@pytest.mark.parametrize("n_pos", [336, 512, 695, 2085])
+def test_decode_mfma_long_splits(ctx, dt, n_pos):
+    """One split per sequence (a split length covering it), so every wave of
+    the MFMA decode runs its tile loop over many tiles: 336 rows give the
+    waves 2-3 full tiles, 512 rows 4 (bf16 / fp16: 8), 695 rows 5-6 and a
+    7-row tail, 2085 rows 16-17 and a 5-row tail; the loop's steady state and
+    each of its drain lengths are taken.  Automatic splits of these short
+    batches give a wave at most one tile."""
+    n_seq = 2
+    q = data(830 + n_pos, (n_seq, NH * HD))
+    kb = store(data(831 + n_pos, (n_seq * n_pos, KVD), 2), dt)
+    vb = store(data(832 + n_pos, (n_seq * n_pos, KVD), 2), dt)
+    dq, dk, dv, dout = ctx.upload(q), ctx.upload(kb), ctx.upload(vb), ctx.empty((n_seq, NH * HD))
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 4096)
+    try:
+        ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, kv_dtype=dt)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+    offs = np.arange(n_seq, dtype=np.int64) * n_pos
+    lens = np.full(n_seq, n_pos, np.int32)
+    ref = oracle.attention_ragged(q, widen(kb, dt), widen(vb, dt), offs, lens, NH, NKV, HD, n_threads=8)
+    assert_close(dout.numpy(), ref, f"dt={dt} {n_seq}x{n_pos} one split")
+    assert ctx.check_device_error() == 0
+
+
 def test_decode_ragged_q8(ctx):
     lens = np.array([1, 0, 513, 4000, 37, 2048, 3], np.int32)
     n_seq = lens.size

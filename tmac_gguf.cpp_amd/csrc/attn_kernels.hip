@@ -2429,7 +2429,7 @@ struct MMath<__bf16> {
     __device__ static float lo(unsigned w) { return __uint_as_float(w << 16); }
     __device__ static float hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
     __device__ static f32x4 mfma32(v8 a, v8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
-    __device__ static f32x4 mfma16(v4 a, v4 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0); }
+    __device__ static v8 cat(v4 a, v4 b) { return __builtin_bit_cast(v8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7)); }
     __device__ static v4 read_tr(char* p) {
         return __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_ptr)p));
     }
@@ -2448,7 +2448,7 @@ struct MMath<_Float16> {
     __device__ static float lo(unsigned w) { return half_bits_to_float(w & 0xffffu); }
     __device__ static float hi(unsigned w) { return half_bits_to_float(w >> 16); }
     __device__ static f32x4 mfma32(v8 a, v8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-    __device__ static f32x4 mfma16(v4 a, v4 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+    __device__ static v8 cat(v4 a, v4 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7); }
     __device__ static v4 read_tr(char* p) {
         return __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_f16x4_ptr)p));
     }
@@ -2710,11 +2710,16 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     }
 
     // LDS: during the tile loop each wave owns a V tile (16-bit, swizzled) and,
-    // for Q8_0, the raw K and V tiles; after it the same bytes hold the
-    // per-wave states for the merge.
+    // for Q8_0, a second V tile (the tile loop is pipelined: one tile's p . v
+    // reads one while the next tile is widened into the other) and the raw K
+    // and V tiles; after it the same bytes hold the per-wave states for the
+    // merge.
     constexpr int VT = kMTileRows * ROWB;
     constexpr int RAWT = Q8 ? MTileQ8<KV>::RAW : 0;
-    constexpr int WAVE_LDS = VT + 2 * RAWT;
+    constexpr bool PIPE = Q8 && NW * (2 * VT + 2 * RAWT) <= 160 * 1024;  // 4 kv heads: 200 KB, not pipelined
+    static_assert(!PIPE || D % 2 == 0, "pipelined tile loop: tile j's V tile is j % 2, fixed per unrolled step");
+    constexpr int NVT = PIPE ? 2 : 1;
+    constexpr int WAVE_LDS = NVT * VT + 2 * RAWT;
     constexpr int NP = NW + (LAYER ? 1 : 0);  // partials merged: the waves, plus the new token in layer modes
     constexpr int MERGE_LDS = NP * NH * kHeadDim * 4 + 2 * NP * NH * 4;
     __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_LDS > MERGE_LDS ? NW * WAVE_LDS : MERGE_LDS];
@@ -2735,7 +2740,7 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
         }
         wr_off[i] = r * ROWB + 16 * (c ^ mswz<KV>(r));
     }
-    char* rk = sv + VT;    // Q8_0: raw K tile
+    char* rk = sv + NVT * VT;  // Q8_0: raw K tile
     char* rv = rk + RAWT;  // Q8_0: raw V tile
     int x_off = 0;         // Q8_0: this lane's remainder chunk, from rk
     if constexpr (Q8) {
@@ -2765,12 +2770,16 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
         return (size_t)page_of(pm, row, bad) * kPageRows * ROWC;
     };
 
-    // One tile: q.k, online softmax, p.v.  `valid` rows of the tile are real.
-    // One tile: q.k, online softmax, p.v.  `valid` rows of the tile are real
-    // (Q8_0: the raw tile is already in LDS when t is null).
-    auto compute = [&](const Tile* t, int valid) {
-        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    // One tile in two stages.  front: V into the V tile `vt`, S^T = K q (rows
+    // past `valid` masked); Q8_0: the raw tile is already in LDS when t is
+    // null.  back: online softmax and O^T += V^T P^T from `vt`.
+    struct Front {
+        f32x4 s;
         f16x2 dv[4];  // Q8_0: V scales (blocks 0, 1 of the own kv head) of this lane's keys 4 g + i
+    };
+    auto front = [&](const Tile* t, int valid, char* vt) -> Front {
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+        f16x2 dv[4] = {};
         if constexpr (Q8) {
             constexpr int RB = MTileQ8<KV>::ROWB;
             if (t) {
@@ -2790,8 +2799,8 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
                 const u32x2 a0 = i8x4_to_bf16(src[0]), a1 = i8x4_to_bf16(src[1]);
                 const u32x2 a2 = i8x4_to_bf16(src[2]), a3 = i8x4_to_bf16(src[3]);
                 const u32x4 w0 = {a0[0], a0[1], a1[0], a1[1]}, w1 = {a2[0], a2[1], a3[0], a3[1]};
-                *reinterpret_cast<u32x4*>(sv + wr_off[2 * i]) = w0;
-                *reinterpret_cast<u32x4*>(sv + wr_off[2 * i + 1]) = w1;
+                *reinterpret_cast<u32x4*>(vt + wr_off[2 * i]) = w0;
+                *reinterpret_cast<u32x4*>(vt + wr_off[2 * i + 1]) = w1;
             }
             // Scales of this lane's keys 4 g + i in its own column's kv head only:
             // the other kv head's S^T entries of the column are exactly 0 (its
@@ -2830,20 +2839,24 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
                 s[i] = __builtin_fmaf((float)dk[i][0], sb[0][i], __builtin_fmaf((float)dk[i][1], sb[1][i], 0.0f));
         } else {
 #pragma unroll
-            for (int i = 0; i < NWR; ++i) *reinterpret_cast<u32x4*>(sv + wr_off[i]) = t->v[i];
+            for (int i = 0; i < NWR; ++i) *reinterpret_cast<u32x4*>(vt + wr_off[i]) = t->v[i];
 #pragma unroll
             for (int b = 0; b < NKB; ++b)
 #pragma unroll
                 for (int part = QP - 1; part >= 0; --part)  // smallest part first
                     s = M::mfma32(t->k[b], qpart[part][b], s);
         }
-        // fp16 queries: s holds S^T times 2^qe; the power of two comes off
-        // the tile max and inside the exp2 argument (exact either way).
         if (valid < kMTileRows) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (4 * g + i >= valid) s[i] = kNegInf;
         }
+        return Front{s, {dv[0], dv[1], dv[2], dv[3]}};
+    };
+    auto back = [&](const Front& f, char* vt) {
+        const f32x4 s = f.s;
+        // fp16 queries: s holds S^T times 2^qe; the power of two comes off
+        // the tile max and inside the exp2 argument (exact either way).
         // Every lane tests its own 4 keys: the column's max exceeds m + kTau
         // exactly when one of its 4 lanes' does, and only then (rare after
         // the first tile) is the column max reduced over the lanes.
@@ -2864,9 +2877,14 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             p[i] = fast_exp2(MQ::kScaleQ ? __builtin_fmaf(s[i], s_unscale, -m) : s[i] - m);  // 0 for masked keys
             l += p[i];
         }
-        // P^T (times kPScale; Q8_0: times the key's V scale of the block) as 16-bit hi + lo
+        // P^T (times kPScale; Q8_0: times the key's V scale of the block) as
+        // 16-bit hi + lo, both in one K = 32 operand: k-slots 8 g .. 8 g + 3
+        // hold this lane's 4 keys' hi parts, 8 g + 4 .. 8 g + 7 their lo parts,
+        // and the V operand repeats the 4 keys' values in both halves (the
+        // order of a contraction's k-slots is free): one 16x16x32 MFMA per
+        // 16-dim block in place of two 16x16x16 ones.
         constexpr int NP = Q8 ? 2 : 1;  // Q8_0: one P' per 32-dim block of the column's own kv head
-        typename M::v4 bh[NP], bl[NP];
+        typename M::v8 pv[NP];
 #pragma unroll
         for (int b = 0; b < NP; ++b) {
             u32x2 ph, pl;
@@ -2874,23 +2892,22 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             for (int i = 0; i < 2; ++i) {
                 float p0 = p[2 * i] * M::kPScale, p1 = p[2 * i + 1] * M::kPScale;
                 if constexpr (Q8) {
-                    p0 = __builtin_fmaf((float)dv[2 * i][b], p0, 0.0f);
-                    p1 = __builtin_fmaf((float)dv[2 * i + 1][b], p1, 0.0f);
+                    p0 = __builtin_fmaf((float)f.dv[2 * i][b], p0, 0.0f);
+                    p1 = __builtin_fmaf((float)f.dv[2 * i + 1][b], p1, 0.0f);
                 }
                 ph[i] = M::pack2(p0, p1);
                 pl[i] = M::pack2(p0 - M::lo(ph[i]), p1 - M::hi(ph[i]));
             }
-            bh[b] = __builtin_bit_cast(typename M::v4, ph);
-            bl[b] = __builtin_bit_cast(typename M::v4, pl);
+            pv[b] = M::cat(__builtin_bit_cast(typename M::v4, ph), __builtin_bit_cast(typename M::v4, pl));
         }
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
-            const typename M::v4 va = M::read_tr(sv + rd_off[mb]);
+            const typename M::v4 va = M::read_tr(vt + rd_off[mb]);
             const int b = Q8 ? (mb & 3) >> 1 : 0;  // Q8_0: 32-dim block of dims 16 mb .. 16 mb + 15 in its kv head
-            acc[mb] = M::mfma16(va, bh[b], acc[mb]);
-            acc[mb] = M::mfma16(va, bl[b], acc[mb]);
+            acc[mb] = M::mfma32(M::cat(va, va), pv[b], acc[mb]);
         }
     };
+    auto compute = [&](const Tile* t, int valid) { back(front(t, valid, sv), sv); };
 
     const int full = n_rows / kMTileRows;
     const int nk = (full - wave + NW - 1) / NW;  // this wave's full tiles: wave + NW * k
@@ -2905,28 +2922,66 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             load(d, min(d, nk - 1));
             __builtin_amdgcn_sched_barrier(0);
         }
-        // Steady state: every prefetch is one of the wave's tiles, so every
-        // iteration issues the same loads and a tile's compute waits only for
-        // that tile's loads (a conditional prefetch makes the compiler wait
-        // for all loads in flight, the D - 1 newer tiles included).  No tile
-        // is fetched twice (a prefetch clamped to the last tile re-read it).
-        int k0 = 0;
-        for (; k0 + 2 * D <= nk; k0 += D) {
+        if constexpr (PIPE) {
+            // Two-stage pipeline: the front of tile j + 1 is issued before
+            // the back of tile j, so the widening, LDS round trips and q . k
+            // MFMAs of one tile overlap the softmax and p . v of the other
+            // (each alone is a chain of dependent steps that two waves per
+            // SIMD do not hide).  Tile j's V tile is j % 2.  Invariant at the
+            // loop head: front(k0) done (st), buf[(k0 + 1 + i) % D] holds tile
+            // k0 + 1 + i for i < D; loads are unconditional here as in the
+            // plain loop below (the first refill is clamped to the last tile).
+            Front st = front(&buf[0], kMTileRows, sv);
+            load(0, min(D, nk - 1));
+            int k0 = 0;
+            for (; k0 + 2 * D < nk; k0 += D) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    const int n = (d + 1) % D;
+                    const Front nx = front(&buf[n], kMTileRows, sv + ((d + 1) & 1) * VT);
+                    load(n, k0 + d + 1 + D);
+                    back(st, sv + (d & 1) * VT);
+                    st = nx;
+                }
+            }
+            // Drain: tiles k0 .. nk - 1 (at most 2 D), front(k0) done.
+#pragma unroll
+            for (int i = 0; i < 2 * D; ++i) {
+                if (k0 + i < nk) {
+                    const int n = (i + 1) % D;
+                    Front nx = st;
+                    if (k0 + i + 1 < nk) {
+                        nx = front(&buf[n], kMTileRows, sv + ((i + 1) & 1) * VT);
+                        if (k0 + i + 1 + D < nk) load(n, k0 + i + 1 + D);
+                    }
+                    back(st, sv + (i & 1) * VT);
+                    st = nx;
+                }
+            }
+        } else {
+            // Steady state: every prefetch is one of the wave's tiles, so every
+            // iteration issues the same loads and a tile's compute waits only for
+            // that tile's loads (a conditional prefetch makes the compiler wait
+            // for all loads in flight, the D - 1 newer tiles included).  No tile
+            // is fetched twice (a prefetch clamped to the last tile re-read it).
+            int k0 = 0;
+            for (; k0 + 2 * D <= nk; k0 += D) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    compute(&buf[d], kMTileRows);
+                    load(d, k0 + d + D);
+                }
+            }
+            // Drain: the last nk - k0 < 2 D tiles.
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                compute(&buf[d], kMTileRows);
-                load(d, k0 + d + D);
+                if (k0 + d < nk) compute(&buf[d], kMTileRows);
+                if (k0 + d + D < nk) load(d, k0 + d + D);
             }
-        }
-        // Drain: the last nk - k0 < 2 D tiles.
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            if (k0 + d < nk) compute(&buf[d], kMTileRows);
-            if (k0 + d + D < nk) load(d, k0 + d + D);
+            for (int d = 0; d < D; ++d)
+                if (k0 + D + d < nk) compute(&buf[d], kMTileRows);
         }
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            if (k0 + D + d < nk) compute(&buf[d], kMTileRows);
     }
     const int tail = n_rows - full * kMTileRows;
     if (tail > 0 && (full % NW) == wave) {
