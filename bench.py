@@ -54,16 +54,31 @@ def algo_bytes(lengths) -> int:
     return int(lengths.sum() * ROW_BYTES + lengths.size * QO_BYTES)
 
 
-def time_launches(ctx, stream, fn, steps: int, warmup: int):
-    """Runs fn() `warmup` times untimed, then exactly `steps` times between two
-    HIP events recorded on `stream` (synchronized before and after): the mean
-    over that region is the step time.  A second, instrumented pass of `steps`
-    launches with an event after each gives the per-launch times for the
-    percentiles (an event per launch adds ~2.6 us per launch at config 3, so it
-    stays out of the mean).  Returns (per-launch ms, mean ms)."""
+# Minimum untimed warm-up of every section besides config 3's headline line
+# (which does exactly --warmup launches): the GPU's clocks rise only after
+# some tens of ms of sustained work, and the compute-heavy kernels follow
+# them (config 3 on a Q8_0 cache: 55.8 us in the first 200 launches after an
+# idle second, 48.1 us from ~30 ms on; fp32 / bf16 caches: 1 %).
+SECTION_WARM_MS = 200.0
+
+
+def time_launches(ctx, stream, fn, steps: int, warmup: int, min_warm_ms: float = SECTION_WARM_MS):
+    """Runs fn() `warmup` times untimed, and more in batches of 20 until at
+    least `min_warm_ms` of wall time has passed since the first, then exactly
+    `steps` times between two HIP events recorded on `stream` (synchronized
+    before and after): the mean over that region is the step time.  A second,
+    instrumented pass of `steps` launches with an event after each gives the
+    per-launch times for the percentiles (an event per launch adds ~2.6 us per
+    launch at config 3, so it stays out of the mean).  Returns (per-launch ms,
+    mean ms)."""
+    t0 = time.perf_counter()
     for _ in range(warmup):
         fn()
     ctx.synchronize(stream)
+    while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
+        for _ in range(20):
+            fn()
+        ctx.synchronize(stream)
     e0, e1 = ctx.event(), ctx.event()
     ctx.record(e0, stream)
     for _ in range(steps):
@@ -99,7 +114,7 @@ def bench_c3(ctx, stream, steps, warmup, n_seq=256, n_pos=4096):
     def launch():
         ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, stream=stream)
 
-    per, mean_ms = time_launches(ctx, stream, launch, steps, warmup)
+    per, mean_ms = time_launches(ctx, stream, launch, steps, warmup, min_warm_ms=0.0)  # exactly W warm-up steps
     out = dout.numpy(stream)
     nbytes = algo_bytes(np.full(n_seq, n_pos))
     res = {
@@ -567,7 +582,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--only-c3", action="store_true", help="time config 3 only (for profiling)")
     ap.add_argument("--rotate", type=int, default=None, help="override TMAC_OPT_ROTATE (tuning)")
@@ -685,6 +700,8 @@ def main():
 
     ctx.destroy_stream(stream)
     ctx.close()
+    if extra:
+        extra["section_warm_ms"] = SECTION_WARM_MS  # minimum untimed warm-up of each extra section
 
     gbs = c3["gbs"]
     line = {

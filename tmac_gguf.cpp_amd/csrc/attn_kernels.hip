@@ -2593,6 +2593,25 @@ __device__ __forceinline__ u32x2 i8x4_to_f16(unsigned w) {
                  __builtin_bit_cast(unsigned, __builtin_bit_cast(f16x2, b) - bias)};
 }
 
+// The 16-value V run lane `lane` widens in step i of a Q8_0 tile: (row, kv
+// head, run in the head, swap).  The lane reads the run's words 2 s, 2 s + 1
+// first (they go to the run's 16-byte V-tile chunk s), then the other two.
+// At 2 kv heads (raw rows of 34 words) each 32-lane half takes rows {e, e + 1,
+// e + 8, e + 9}, 8 lanes per row, and swaps the second kv head's runs: the
+// raw words of each read then fall in 32 distinct banks, and each 8 lanes'
+// 16-byte V-tile writes in 8 distinct bank groups (the plain order, 8 lanes
+// per row for rows 0..7 and 8..15, conflicts 2-way on both).
+template <int KV>
+__device__ __forceinline__ int4 q8_vrun(int i, int lane) {
+    if constexpr (KV == 2) {
+        const int hg = 2 * i + lane / 32, gi = (lane % 32) / 8, h = (lane / 4) % 2;
+        return int4{2 * hg + (gi & 1) + 8 * (gi >> 1), h, lane % 4, h};
+    } else {
+        const int q = 64 * i + lane;
+        return int4{q / (4 * KV), (q / 4) % KV, q % 4, 0};
+    }
+}
+
 // Element type -> MFMA operand type, tile, and cache row bytes.
 template <typename T, int KV>
 struct MTraits {
@@ -2726,13 +2745,16 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
     char* sv = smem + wave * WAVE_LDS;
     constexpr int NWR = Q8 ? 2 * MTileQ8<KV>::NVU : MTile<__bf16, KV>::NV;  // 16-byte LDS writes per lane
     int wr_off[NWR];
+    int vrd_off[NWR];  // Q8_0: raw V byte offsets of the words widened into V-tile write i
 #pragma unroll
     for (int i = 0; i < NWR; ++i) {
         int r, c;
-        if (Q8) {  // run i / 2 of 16 values: row q / (4 KV), kv head (q / 4) % KV, 16-value run q % 4
-            const int q = 64 * (i / 2) + lane;
-            r = q / (4 * KV);
-            c = 8 * ((q / 4) % KV) + 2 * (q % 4) + (i & 1);
+        if (Q8) {  // write i: chunk (i & 1) ^ swap of run i / 2 (q8_vrun)
+            const int4 u = q8_vrun<KV>(i / 2, lane);
+            const int half = (i & 1) ^ u.w;
+            r = u.x;
+            c = 8 * u.y + 2 * u.z + half;
+            vrd_off[i] = r * MTileQ8<KV>::ROWB + u.y * kQ8HeadBytes + 16 * u.z + 8 * half;
         } else {
             const int q = 64 * i + lane;
             r = q / CPR;
@@ -2794,10 +2816,10 @@ __device__ __forceinline__ void mdecode_segment(const DecodeArgs& a, int seq, in
             }
 #pragma unroll
             for (int i = 0; i < MTileQ8<KV>::NVU; ++i) {  // V runs: widen to bf16, into the V tile
-                const int q = 64 * i + lane, r = q / (4 * KV), h = (q / 4) % KV, ck = q % 4;
-                const unsigned* src = reinterpret_cast<const unsigned*>(rv + r * RB + h * kQ8HeadBytes + 16 * ck);
-                const u32x2 a0 = i8x4_to_bf16(src[0]), a1 = i8x4_to_bf16(src[1]);
-                const u32x2 a2 = i8x4_to_bf16(src[2]), a3 = i8x4_to_bf16(src[3]);
+                const unsigned* sa = reinterpret_cast<const unsigned*>(rv + vrd_off[2 * i]);
+                const unsigned* sb = reinterpret_cast<const unsigned*>(rv + vrd_off[2 * i + 1]);
+                const u32x2 a0 = i8x4_to_bf16(sa[0]), a1 = i8x4_to_bf16(sa[1]);
+                const u32x2 a2 = i8x4_to_bf16(sb[0]), a3 = i8x4_to_bf16(sb[1]);
                 const u32x4 w0 = {a0[0], a0[1], a1[0], a1[1]}, w1 = {a2[0], a2[1], a3[0], a3[1]};
                 *reinterpret_cast<u32x4*>(vt + wr_off[2 * i]) = w0;
                 *reinterpret_cast<u32x4*>(vt + wr_off[2 * i + 1]) = w1;
