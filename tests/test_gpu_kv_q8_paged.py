@@ -406,6 +406,35 @@ def test_decode_paged(ctx, dt, hint):
     assert ctx.check_device_error() == 0
 
 
+@pytest.mark.parametrize("dt", [tmac_attn.TMAC_KV_BF16, Q8])
+def test_decode_paged_long_splits(ctx, dt):
+    """Paged MFMA decode with one split per sequence: every wave walks many
+    pages through the tile loop's steady state and drain (lengths as in the
+    contiguous long-split test, plus one page exactly)."""
+    lens = np.array([336, 512, 695, 2085, 16], np.int32)
+    n_seq = lens.size
+    k_rows = [store(data(860 + s, (int(lens[s]), KVD), 2), dt) for s in range(n_seq)]
+    v_rows = [store(data(870 + s, (int(lens[s]), KVD), 2), dt) for s in range(n_seq)]
+    n_pages = int(sum((l + PR - 1) // PR for l in lens)) + 5
+    kp, table = build_pool(k_rows, dt, n_pages, np.random.default_rng(11))
+    vp, _ = build_pool(v_rows, dt, n_pages, np.random.default_rng(11))
+    q = data(880 + dt, (n_seq, NH * HD))
+    dq, dk, dv, dt_, dl = ctx.upload(q), ctx.upload(kp), ctx.upload(vp), ctx.upload(table), ctx.upload(lens)
+    dout = ctx.empty((n_seq, NH * HD))
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 4096)
+    try:
+        ctx.decode_paged(dq, dk, dv, n_pages, dt_, table.shape[1], dl, dout, n_seq, NH, NKV, HD, int(lens.max()),
+                         kv_dtype=dt)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+    kw = np.concatenate([widen(r, dt) for r in k_rows])
+    vw = np.concatenate([widen(r, dt) for r in v_rows])
+    offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
+    ref = oracle.attention_ragged(q, kw, vw, offs, lens, NH, NKV, HD, n_threads=8)
+    assert_close(dout.numpy(), ref, f"paged long splits dt={dt}")
+    assert ctx.check_device_error() == 0
+
+
 def test_decode_paged_shared_prefix_and_splits(ctx):
     """Two sequences sharing their first 40 pages; a forced short split length
     so that every sequence spans many workgroups and the combine kernel runs."""
