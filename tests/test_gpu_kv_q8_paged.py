@@ -148,6 +148,47 @@ def test_decode_ragged_q8(ctx):
     assert ctx.check_device_error() == 0
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_decode_ragged_random_cases(ctx, seed):
+    """Seeded random ragged batches on every cache type: 1-6 sequences of
+    0-3000 rows at gapped offsets, a random split length (automatic, 16 to
+    4096 rows) and schedule (unit grid, automatic, stream-K), with and without
+    the total_rows hint."""
+    rng = np.random.default_rng(1000 + seed)
+    dt = ALL_DT[seed % len(ALL_DT)]
+    n_seq = int(rng.integers(1, 7))
+    lens = rng.integers(0, 3001, n_seq).astype(np.int32)
+    lens[rng.random(n_seq) < 0.15] = 0
+    gaps = rng.integers(0, 40, n_seq)
+    offs = (np.concatenate([[0], np.cumsum(lens[:-1])]) + np.cumsum(gaps)).astype(np.int64)
+    rows = int(offs[-1] + lens[-1]) + 1
+    split_len = int(rng.choice([0, 16, 48, 256, 4096]))
+    stream_k = int(rng.choice([0, 1, 2]))
+    hint = int(lens.sum()) if rng.random() < 0.5 else 0
+    q = data(1100 + seed, (n_seq, NH * HD)) * np.float32(rng.choice([0.25, 1.0, 4.0]))
+    kb = store(data(1200 + seed, (rows, KVD), 2), dt)
+    vb = store(data(1300 + seed, (rows, KVD), 2), dt)
+    dq, dk, dv = ctx.upload(q), ctx.upload(kb), ctx.upload(vb)
+    doffs, dlens, dout = ctx.upload(offs), ctx.upload(lens), ctx.empty((n_seq, NH * HD))
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, split_len)
+    ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, stream_k)
+    try:
+        ctx.decode_ragged(dq, dk, dv, doffs, dlens, dout, n_seq, NH, NKV, HD, max(int(lens.max()), 1), hint,
+                          kv_dtype=dt)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 1)
+    what = f"seed {seed}: dt={dt} lens={lens.tolist()} split={split_len} stream_k={stream_k} hint={hint}"
+    got = dout.numpy()
+    nz = lens > 0
+    assert np.all(got[~nz] == 0), what
+    if nz.any():
+        ref = oracle.attention_ragged(q[nz], widen(kb, dt), widen(vb, dt), offs[nz], lens[nz], NH, NKV, HD,
+                                      n_threads=8)
+        assert_close(got[nz], ref, what)
+    assert ctx.check_device_error() == 0, what
+
+
 @pytest.mark.parametrize("pos,kernel", [(0, 0), (200, 0), (1500, tmac_attn.TMAC_KERNEL_GROUP),
                                         (90, tmac_attn.TMAC_KERNEL_HEAD), (3000, 0)])
 def test_layer_step_q8(ctx, pos, kernel):
