@@ -213,6 +213,54 @@ def test_layer_step_q8(ctx, pos, kernel):
     assert_close(dout.numpy(), ref, f"layer q8 pos={pos}")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_layer_step_random_cases(ctx, seed):
+    """Seeded random fused layer steps on every cache type: position (0, short
+    or long), RoPE base, kernel choice (automatic, group, head, split-V head),
+    MFMA or VALU decode, forced split length, and the position passed by value
+    or in a device counter.  The cache rows are checked bit for bit and the
+    output against the oracle's layer step."""
+    rng = np.random.default_rng(2000 + seed)
+    dt = ALL_DT[seed % len(ALL_DT)]
+    pos = int(rng.choice([0, int(rng.integers(1, 64)), int(rng.integers(64, 5000))]))
+    cap = pos + int(rng.integers(1, 40))
+    base = float(rng.choice([1e4, 1e6]))
+    kernel = int(rng.choice([tmac_attn.TMAC_KERNEL_AUTO, tmac_attn.TMAC_KERNEL_GROUP, tmac_attn.TMAC_KERNEL_HEAD,
+                             tmac_attn.TMAC_KERNEL_HEADV]))
+    mfma = int(rng.integers(0, 2))
+    split_len = int(rng.choice([0, 0, 32, 256]))
+    devpos = bool(rng.integers(0, 2))
+    q, kn, vn = data(2100 + seed, NH * HD), data(2200 + seed, KVD), data(2300 + seed, KVD)
+    kb = store(data(2400 + seed, (cap, KVD), 2), dt)
+    vb = store(data(2500 + seed, (cap, KVD), 2), dt)
+    dq, dkn, dvn = ctx.upload(q), ctx.upload(kn), ctx.upload(vn)
+    dk, dv, dout = ctx.upload(kb), ctx.upload(vb), ctx.empty(NH * HD)
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, kernel)
+    ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, mfma)
+    ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, split_len)
+    try:
+        if devpos:
+            dpos = ctx.upload(np.array([pos], np.int32))
+            ctx.layer_attention_devpos(dq, dkn, dvn, dk, dv, dout, NH, NKV, HD, dpos, cap, base, kv_dtype=dt)
+        else:
+            ctx.layer_attention(dq, dkn, dvn, dk, dv, dout, NH, NKV, HD, pos, cap, base, kv_dtype=dt)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, 0)
+        ctx.set_option(tmac_attn.TMAC_OPT_MFMA_DECODE, 1)
+        ctx.set_option(tmac_attn.TMAC_OPT_SPLIT_LEN, 0)
+    what = (f"seed {seed}: dt={dt} pos={pos} cap={cap} base={base} kernel={kernel} mfma={mfma} "
+            f"split={split_len} devpos={devpos}")
+    qr, kr = oracle.rope(q, kn, NH, NKV, HD, pos, base)
+    kb_ref, vb_ref = kb.copy(), vb.copy()
+    kb_ref[pos] = store(kr, dt)[0]
+    vb_ref[pos] = store(vn, dt)[0]
+    np.testing.assert_array_equal(dk.numpy(), kb_ref, err_msg=what)
+    np.testing.assert_array_equal(dv.numpy(), vb_ref, err_msg=what)
+    ref = oracle.attention(qr, widen(kb_ref, dt), widen(vb_ref, dt), NH, NKV, HD, pos)
+    assert_close(dout.numpy(), ref, what)
+    assert ctx.check_device_error() == 0, what
+
+
 def rows_of(x: np.ndarray, dt: int, rb: int) -> np.ndarray:
     """fp32 values -> stored cache rows of rb elements, for any number of kv heads."""
     flat = np.ascontiguousarray(x, np.float32).reshape(-1)
