@@ -320,3 +320,20 @@ def test_prefill_graph_replay_matches_eager(ctx):
     finally:
         ctx.graph_destroy(g)
         ctx.destroy_stream(s)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_prefill_random_cases(ctx, seed):
+    """Seeded random chunked prefills: 1-3 sequences, 1-200 queries after a
+    0-700-row prefix, spare capacity, and a GQA shape drawn from the compiled
+    ones, on bf16-exact inputs (the kernel's operands are then the inputs)."""
+    rng = np.random.default_rng(3000 + seed)
+    n_head, n_kv = [(14, 2), (16, 4), (8, 1), (2, 2), (1, 1), (4, 2)][seed % 6]
+    n_seq = int(rng.integers(1, 4))
+    n_q = int(rng.integers(1, 201))
+    prefix = int(rng.choice([0, int(rng.integers(1, 64)), int(rng.integers(64, 701))]))
+    cap = prefix + n_q + int(rng.integers(0, 30))
+    q, k, v = (bf16_round(a) for a in make(3100 + 10 * seed, n_seq, n_q, prefix, cap, n_head, n_kv))
+    got = run(ctx, q, k, v, n_seq, n_q, prefix, cap, n_head, n_kv)
+    ref = oracle.prefill(q, k, v, n_seq, n_q, prefix, cap, n_head, n_kv, HD, n_threads=8)
+    assert_close(got, ref, f"seed {seed}: {n_seq}x{n_q} prefix {prefix} cap {cap} heads {n_head}/{n_kv}")
