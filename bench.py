@@ -469,6 +469,16 @@ def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
         ctx.prefill_tiles(dq, tiles, cap, dout2, n_seq, n_q, prefix, NH, NKV, HD, stream=stream)
 
     per_c, mean_c = time_launches(ctx, stream, chunk, steps, warmup)
+    # The same chunk call (pack + attention) 10 times in one captured graph, as
+    # a serving loop issues it: GPU time per call without the eager launch gaps.
+    n_g = 10
+    ctx.step_begin(stream)
+    for _ in range(n_g):
+        chunk()
+    g = ctx.step_end(stream)
+    _, mean_g = time_launches(ctx, stream, lambda: ctx.graph_launch(g, stream), max(5, steps // 5), 5)
+    ctx.graph_destroy(g)
+    mean_g /= n_g
     same = bool(np.array_equal(dout.numpy().view(np.uint32), dout2.numpy().view(np.uint32)))
     for d in (dq, dk, dv, dout, dout2, tiles):
         d.free()
@@ -478,11 +488,14 @@ def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
             "tflops": tflops, "mfma_util": tflops / MFMA_BF16_PEAK_TFLOPS,
             "repack_all_mean_us": mean_ms * 1e3, "repack_all_median_us": float(np.median(per)) * 1e3,
             "repack_all_mfma_util": tflops_full / MFMA_BF16_PEAK_TFLOPS,
+            "graph_mean_us": mean_g * 1e3,
+            "graph_mfma_util": C5_FLOPS / (mean_g * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
             "chunk_equals_repack_all": same,
             "bytes": n_seq * n_q * NH * HD * 4 * 2 + n_seq * cap * KVD * 4 * 2,
             "note": "mean_us / mfma_util: one chunk of the chunked flow (pack the chunk's 512 rows into the "
                     "persistent bf16 tile copy, attention over the tiles; the 1536 prefix rows packed by the "
-                    "earlier chunks); repack_all_*: tmac_attention_prefill, which packs all 2048 rows per call"}
+                    "earlier chunks); repack_all_*: tmac_attention_prefill, which packs all 2048 rows per call; "
+                    "graph_*: the chunk call 10 times in one captured graph, time per call"}
 
 
 def _cpu_facts():
@@ -685,7 +698,8 @@ def main():
         c5 = extra["c5"]
         log(f"[bench] C5 chunk {c5['mean_us']:.1f} us, {c5['tflops']:.1f} TFLOP/s, MFMA util "
             f"{c5['mfma_util'] * 100:.2f}%; repack-all call {c5['repack_all_mean_us']:.1f} us "
-            f"({c5['repack_all_mfma_util'] * 100:.2f}%); equal outputs: {c5['chunk_equals_repack_all']}")
+            f"({c5['repack_all_mfma_util'] * 100:.2f}%); in a graph {c5['graph_mean_us']:.1f} us "
+            f"({c5['graph_mfma_util'] * 100:.2f}%); equal outputs: {c5['chunk_equals_repack_all']}")
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
