@@ -40,6 +40,11 @@
  *    other n_head a multiple of n_kv_head and any even head_dim up to 256
  *    (one workgroup per query head; scores scaled by 1/sqrt(head_dim)), and
  *    tmac_rope_op / tmac_rope_rows any even head_dim up to 256 (kernel_rope.metal:5-22).
+ *    The reference's kernel_attn is one 32-lane simdgroup with 2 dims per lane
+ *    (kernel_attn.metal:20-21), so it defines head_dim <= 64 only; above 64 this
+ *    library computes attention over every dimension, as the CPU restatement
+ *    of tmac_gguf.cpp:1093-1128 generalised to head_dim does, with no reference
+ *    result to compare against (parity there is unpinned).
  *    The bf16 / fp16 / Q8_0 caches, the paged caches and chunked prefill keep
  *    head_dim 64 and the compiled groups; other shapes return TMAC_ERR_UNSUPPORTED.
  */
@@ -358,10 +363,10 @@ int tmac_attention_prefill_paged(tmac_context* ctx, tmac_stream stream, int kv_d
  * bytes for `capacity` rows per sequence (16 KiB per 64 rows and (sequence, kv head),
  * rows rounded up to 256); it is valid for the rows packed so far and the caller keeps
  * it in step with the cache (repack rows that change).
- *   tmac_prefill_pack_rows: packs rows row_begin .. row_end - 1 of every sequence (whole
- *     64-row tiles: rows below row_end from the cache, the rest of the last tile zero).
- *     Cache layout and kv_dtype as tmac_attention_prefill_kv; row_end <= capacity,
- *     seq_stride >= capacity when n_seq > 1.
+ *   tmac_prefill_pack_rows: packs rows row_begin .. row_end - 1 of every sequence, in any
+ *     order and any number of times (a middle range that changed can be repacked); the
+ *     other rows of the tiles keep their contents.  Cache layout and kv_dtype as
+ *     tmac_attention_prefill_kv; row_end <= capacity, seq_stride >= capacity when n_seq > 1.
  *   tmac_attention_prefill_tiles: the attention of tmac_attention_prefill over the tiles,
  *     which must hold rows 0 .. prefix_len + n_q - 1 (prefix_len + n_q <= capacity).
  * pack_rows(0, prefix_len + n_q) then attention_prefill_tiles gives the outputs of

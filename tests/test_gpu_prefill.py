@@ -264,6 +264,52 @@ def test_prefill_tiles_chunks_match_full_call(ctx, dt):
     assert ctx.check_device_error() == 0
 
 
+def test_prefill_tiles_repack_middle_range_and_unwritten_rows(ctx):
+    """tmac_prefill_pack_rows writes only the rows it is given.  The tile buffer
+    starts as all-ones bytes (every bf16 a NaN): (1) after packing only rows
+    0..129, a chunk ending at row 130 reads tile 2, whose rows 130..191 were never
+    written, and still equals tmac_attention_prefill bit for bit; (2) with every
+    row packed back to front, cache rows 100..109 are then changed and only they
+    are repacked, and chunks ending past row 110 (which reads tile 1's rows
+    110..127, packed earlier) equal tmac_attention_prefill on the changed cache bit
+    for bit and the oracle within the fp32 tolerance."""
+    n_seq, nh, nkv, cap = 2, 14, 2, 300
+    q, k, v = (bf16_round(a) for a in make(990, n_seq, cap, 0, cap, nh, nkv))
+    dk, dv = ctx.upload(k), ctx.upload(v)
+    tiles = ctx.empty(ctx.prefill_tiles_bytes(n_seq, nkv, cap), np.uint8)
+    tiles.fill_bytes(0xFF)
+
+    def check(c0, c1, kk, vv, what):
+        n = c1 - c0
+        dq = ctx.upload(np.ascontiguousarray(q[:, c0:c1]))
+        out_t, out_f = ctx.empty((n_seq, n, nh * HD)), ctx.empty((n_seq, n, nh * HD))
+        ctx.prefill_tiles(dq, tiles, cap, out_t, n_seq, n, c0, nh, nkv, HD)
+        ctx.prefill(dq, dk, dv, out_f, n_seq, n, c0, cap, nh, nkv, HD)
+        got = out_t.numpy()
+        assert np.all(np.isfinite(got)), what
+        np.testing.assert_array_equal(got.view(np.uint32), out_f.numpy().view(np.uint32), err_msg=what)
+        ref = oracle.prefill(np.ascontiguousarray(q[:, c0:c1]), kk, vv, n_seq, n, c0, cap, nh, nkv, HD, n_threads=8)
+        assert_close(got, ref, what)
+        for d in (dq, out_t, out_f):
+            d.free()
+
+    ctx.prefill_pack_rows(dk, dv, cap, tiles, cap, n_seq, nkv, HD, 0, 130)
+    check(100, 130, k, v, "rows 130..191 of tile 2 never packed")
+    for r0, r1 in ((250, 300), (130, 250), (0, 130)):  # back to front
+        ctx.prefill_pack_rows(dk, dv, cap, tiles, cap, n_seq, nkv, HD, r0, r1)
+    k2, v2 = k.copy(), v.copy()
+    k2[:, 100:110] = bf16_round(oracle.normal(995, (n_seq, 10, nkv * HD)) * 3)
+    v2[:, 100:110] = bf16_round(oracle.normal(996, (n_seq, 10, nkv * HD)))
+    dk.copy_from(k2)
+    dv.copy_from(v2)
+    ctx.prefill_pack_rows(dk, dv, cap, tiles, cap, n_seq, nkv, HD, 100, 110)
+    for c0, c1 in ((0, 300), (105, 140), (120, 128)):
+        check(c0, c1, k2, v2, f"chunk {c0}..{c1} after rows 100..109 were repacked")
+    for d in (dk, dv, tiles):
+        d.free()
+    assert ctx.check_device_error() == 0
+
+
 def test_prefill_tiles_rejects_bad_arguments(ctx):
     import tmac_attn
     d = ctx.empty(4096)

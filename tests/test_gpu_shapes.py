@@ -108,6 +108,60 @@ def test_layer_step_any_shape(ctx, nh, nkv, hd):
     assert ctx.check_device_error() == 0
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(2, 1, 2), (14, 2, 32), (14, 2, 128)])
+def test_layer_step_any_shape_counter_far_positions(ctx, nh, nkv, hd):
+    """A device-side position counter read by the any-shape layer step and moved by
+    tmac_pos_update (set, then advanced by one) to positions far past rows * hd / 64
+    of a 4096-row RoPE table (127 for hd 2, 2047 for hd 32), up to the last row.  The
+    counter first serves a head_dim-64 layer step (whose kernel keeps the counter's
+    cached RoPE row), so the advances also refresh that cache from the head_dim-64
+    table.  Both layer steps match the oracle (tmac_gguf.cpp:1085-1128) at every
+    position, the cache rows bit-exact, and no device error is raised."""
+    cap = 4096
+    kc = oracle.normal(7600 + hd, (cap, nkv * hd))
+    vc = oracle.normal(7601 + hd, (cap, nkv * hd))
+    k64 = oracle.normal(7602, (cap, 128))
+    v64 = oracle.normal(7603, (cap, 128))
+    dkc, dvc, dout = ctx.upload(kc), ctx.upload(vc), ctx.empty(nh * hd)
+    dk64, dv64, dout64 = ctx.upload(k64), ctx.upload(v64), ctx.empty(14 * 64)
+    pos_dev = ctx.upload(np.zeros(1, np.int32))
+    ctx.rope_prepare(hd, 1e6, cap)
+    ctx.rope_prepare(64, 1e6, cap)
+    s = ctx.stream()
+    try:
+        for i, (pos, how) in enumerate([(0, "set"), (126, "set"), (127, "add"), (128, "add"), (2046, "set"),
+                                        (2047, "add"), (2048, "add"), (4094, "set"), (4095, "add")]):
+            if how == "set":
+                ctx.pos_update(pos_dev, pos, stream=s)
+            else:
+                ctx.pos_update(pos_dev, 1, add=True, stream=s)
+            q64 = oracle.normal(7610 + i, 14 * 64)
+            kn64, vn64 = oracle.normal(7620 + i, 128), oracle.normal(7630 + i, 128)
+            q = oracle.normal(7640 + i, nh * hd)
+            kn, vn = oracle.normal(7650 + i, nkv * hd), oracle.normal(7660 + i, nkv * hd)
+            dq64, dkn64, dvn64 = ctx.upload(q64), ctx.upload(kn64), ctx.upload(vn64)
+            dq, dkn, dvn = ctx.upload(q), ctx.upload(kn), ctx.upload(vn)
+            ctx.layer_attention_devpos(dq64, dkn64, dvn64, dk64, dv64, dout64, 14, 2, 64, pos_dev, cap, 1e6,
+                                       stream=s)
+            ctx.layer_attention_devpos(dq, dkn, dvn, dkc, dvc, dout, nh, nkv, hd, pos_dev, cap, 1e6, stream=s)
+            ctx.synchronize(s)
+            assert int(pos_dev.numpy()[0]) == pos
+            ref64, _, _ = oracle.layer_step(q64, kn64, vn64, k64, v64, 14, 2, 64, pos, 1e6)
+            ref, _, _ = oracle.layer_step(q, kn, vn, kc, vc, nh, nkv, hd, pos, 1e6)
+            assert_close(dout64.numpy(), ref64, f"head_dim 64 layer step at pos {pos}")
+            assert_close(dout.numpy(), ref, f"layer {nh}/{nkv}/{hd} pos {pos} ({how})")
+            assert ctx.check_device_error() == 0, f"device error at pos {pos}"
+            for d in (dq64, dkn64, dvn64, dq, dkn, dvn):
+                d.free()
+        np.testing.assert_array_equal(dkc.numpy(), kc)
+        np.testing.assert_array_equal(dvc.numpy(), vc)
+        np.testing.assert_array_equal(dk64.numpy(), k64)
+    finally:
+        ctx.destroy_stream(s)
+        for d in (dkc, dvc, dout, dk64, dv64, dout64, pos_dev):
+            d.free()
+
+
 def test_other_entry_points_refuse_other_shapes(ctx):
     U = tmac_attn.TMAC_ERR_UNSUPPORTED
     d = ctx.empty(1 << 16)

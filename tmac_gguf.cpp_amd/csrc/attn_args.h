@@ -101,7 +101,7 @@ struct PrefillArgs {
     float qscale;            // log2(e) / sqrt(head_dim)
     uint16_t* packed;        // bf16 tiles [n_seq][n_kv_head][n_tp][K tile, V^T tile] (64 x 64 each)
     int n_tp;                // tiles per (sequence, kv head): ceil(rows / 64) rounded up to a stage
-    int n_rows;              // pack: rows below this are cache rows, the rest of a tile is zero
+    int n_rows;              // pack: rows row_lo .. n_rows - 1 are written; other rows keep their contents
     int tile0;               // pack: first tile of every (sequence, kv head) this launch packs
     int n_tpp;               // pack: tiles per (sequence, kv head) this launch packs
     // paged caches: k / v are pools of n_pages kPageRows-row pages, sequence s's
@@ -110,6 +110,7 @@ struct PrefillArgs {
     int max_pages;
     int n_pages;
     int* err;                // bit 2: a block-table entry outside the pool (clamped)
+    int row_lo;              // pack: first row written
 };
 constexpr int kPrefillQueries = 16;  // queries per workgroup (one MFMA column block)
 constexpr int kPrefillKeys = 64;     // keys per tile

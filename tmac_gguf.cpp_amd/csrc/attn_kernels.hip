@@ -2016,8 +2016,11 @@ __device__ __forceinline__ float sum4_rows(float v) {
 // threads, thread t owns row t / 4 and the 8-dim chunks q4 and 4 + q4
 // (q4 = t % 4) of the K tile and of the V^T tile.  Values are widened exactly
 // to fp32 (load_row) and rounded to bf16 (nearest even; exact for a bf16
-// cache).  Rows at or past n_rows are written as zeros.  A launch packs the
-// tiles tile0 .. tile0 + n_tpp - 1 of every (sequence, kv head).
+// cache).  Only rows row_lo .. n_rows - 1 are written: the other rows of a
+// tile keep what an earlier pack left there (the attention kernel reads no
+// row past the last query's key, so rows never packed may hold anything).
+// A launch packs the tiles tile0 .. tile0 + n_tpp - 1 of every (sequence,
+// kv head).
 template <typename T, int KV, bool PAGED>
 __device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
     constexpr int HB = CacheFmt<T>::kHeadBytes, ROWB = KV * HB, DB = CacheFmt<T>::kDimBytes;
@@ -2040,7 +2043,7 @@ __device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
     }
     const char* kh = reinterpret_cast<const char*>(a.k) + row * ROWB + kv * HB;
     const char* vh = reinterpret_cast<const char*>(a.v) + row * ROWB + kv * HB;
-    const bool valid = key < a.n_rows;
+    const bool valid = key >= a.row_lo && key < a.n_rows;
     __shared__ float sv[64][65];
     // load_row(c) gives dims 4c..4c+3 and 32+4c..32+4c+3; c = 2 q4 and 2 q4 + 1
     // together hold the chunks 8 q4 .. 8 q4 + 7 and 32 + 8 q4 .. 32 + 8 q4 + 7.
@@ -2063,23 +2066,43 @@ __device__ __forceinline__ void prefill_pack_body(const PrefillArgs& a) {
     }
     __bf16* dst = reinterpret_cast<__bf16*>(a.packed) +
                   (((size_t)seq * KV + kv) * a.n_tp + tile) * kPrefillTileElems;
+    if (valid) {
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-        const float* x = kx[cc];
-        const u32x4 w = {bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3]), bf16_pair(x[4], x[5]),
-                         bf16_pair(x[6], x[7])};
-        *reinterpret_cast<u32x4*>(dst + tile_offset(r, 32 * cc + 8 * q4)) = w;
+        for (int cc = 0; cc < 2; ++cc) {
+            const float* x = kx[cc];
+            const u32x4 w = {bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3]), bf16_pair(x[4], x[5]),
+                             bf16_pair(x[6], x[7])};
+            *reinterpret_cast<u32x4*>(dst + tile_offset(r, 32 * cc + 8 * q4)) = w;
+        }
     }
     __syncthreads();
-    // V^T row d = r, columns p = 16 * q4 .. + 15 hold keys vt_key(p)
+    // V^T row d = r, columns p = 16 * q4 .. + 15 hold keys vt_key(p).  A chunk
+    // whose 8 keys straddle row_lo or n_rows keeps the old values of the keys
+    // outside (read back and merged per 16-bit element).
+    const int tkey0 = tile * kPrefillKeys;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
         float x[8];
+        unsigned keep = 0;  // bit e: key e of the chunk lies outside row_lo .. n_rows - 1
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sv[vt_key(16 * q4 + 8 * cc + e)][r];
-        const u32x4 w = {bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3]), bf16_pair(x[4], x[5]),
-                         bf16_pair(x[6], x[7])};
-        *reinterpret_cast<u32x4*>(dst + 64 * 64 + tile_offset(r, 16 * q4 + 8 * cc)) = w;
+        for (int e = 0; e < 8; ++e) {
+            const int kk = vt_key(16 * q4 + 8 * cc + e);
+            x[e] = sv[kk][r];
+            keep |= (tkey0 + kk < a.row_lo || tkey0 + kk >= a.n_rows) ? 1u << e : 0u;
+        }
+        u32x4 w = {bf16_pair(x[0], x[1]), bf16_pair(x[2], x[3]), bf16_pair(x[4], x[5]), bf16_pair(x[6], x[7])};
+        u32x4* p = reinterpret_cast<u32x4*>(dst + 64 * 64 + tile_offset(r, 16 * q4 + 8 * cc));
+        if (keep == 0xFFu) continue;
+        if (keep) {
+            const u32x4 old = *p;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned mk = ((keep >> (2 * i)) & 1u ? 0x0000FFFFu : 0u) |
+                                    ((keep >> (2 * i + 1)) & 1u ? 0xFFFF0000u : 0u);
+                w[i] = (w[i] & ~mk) | (old[i] & mk);
+            }
+        }
+        *p = w;
     }
 }
 
@@ -2235,6 +2258,24 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) va[db][j] = *reinterpret_cast<const bf16x8*>(tv + op_off[db][j]);
+            // Keys past the block's last query are rows a pack need not have
+            // written: their weights are 0, and their V is set to 0 so that no
+            // NaN or infinity left there reaches the product.
+            const int vlim = kmax - kbase - KT * u;  // keys of tile u above vlim (wave-uniform)
+            if (diag && vlim < KT - 1) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    u32x4 keep;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        const int p0 = 32 * j + 8 * g4 + 2 * w;
+                        keep[w] = (vt_key(p0) <= vlim ? 0x0000FFFFu : 0u) | (vt_key(p0 + 1) <= vlim ? 0xFFFF0000u : 0u);
+                    }
+#pragma unroll
+                    for (int db = 0; db < 4; ++db)
+                        va[db][j] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, va[db][j]) & keep);
+                }
+            }
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 // P^T operands for PV K-step j: keys 32j + 16h + 4*g4 + i  <->  S^T block 2j + h, row i

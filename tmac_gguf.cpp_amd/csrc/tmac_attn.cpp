@@ -1026,7 +1026,13 @@ static int layer_common(tmac_context* ctx, hipStream_t stream, const float* q, c
     a.rope_cs = rt->dev;
     a.rope_rows = rt->rows;
     a.pos_dev = pos_dev;
-    a.pos_slots = pos_dev ? pos_slots_for(ctx, pos_dev) : nullptr;
+    // The row cache holds head_dim-64 rows (32 cos/sin pairs), which is what
+    // tmac_pos_update copies and what the compiled kernels read.  The
+    // any-shape kernel (any other head_dim) reads its table directly, and its
+    // table is not recorded for the counter: a copy of 32 pairs from a table
+    // of shorter rows would read past it.
+    const bool row_cache = pos_dev && !kern.any && head_dim == kHeadDim;
+    a.pos_slots = row_cache ? pos_slots_for(ctx, pos_dev) : nullptr;
     if (a.pos_slots) ctx->pos_table_of[pos_dev] = {rt->dev, rt->rows};
     a.pos_host = pos;
     a.capacity = capacity;
@@ -1225,7 +1231,7 @@ static int prefill_impl(tmac_context* ctx, tmac_stream stream, int dt, const flo
     if ((rc = ensure_workspace(ctx, (hipStream_t)stream, pack_bytes / sizeof(float)))) return rc;
     PrefillArgs a{q, static_cast<const float*>(k_cache), static_cast<const float*>(v_cache), out, seq_stride, n_q,
                   prefix_len, n_qblk, kQScale, reinterpret_cast<uint16_t*>(workspace(ctx)), n_tp, n_rows, 0, n_tp,
-                  block_table, max_pages, n_pages, ctx->err};
+                  block_table, max_pages, n_pages, ctx->err, 0};
     if ((rc = launch(ctx, ctx->prefill_pack[block_table ? 1 : 0][dt].at(n_kv_head), (unsigned)pack_blocks, 1, 256,
                      (hipStream_t)stream, &a)))
         return rc;
@@ -1297,10 +1303,11 @@ int tmac_prefill_pack_rows(tmac_context* ctx, tmac_stream stream, int kv_dtype, 
     if (blocks > INT_MAX || (int64_t)n_tp * n_kv_head * n_seq > INT_MAX)
         return fail(ctx, TMAC_ERR_INVALID_ARG, "prefill_pack_rows: too many cache tiles");
     if ((rc = set_device(ctx))) return rc;
-    // Whole tiles t0 .. t1 - 1: rows below row_end from the cache, the rest zero.
+    // Tiles t0 .. t1 - 1, rows row_begin .. row_end - 1 from the cache; the
+    // other rows of those tiles keep their contents.
     PrefillArgs a{nullptr, static_cast<const float*>(k_cache), static_cast<const float*>(v_cache), nullptr,
                   seq_stride, 0, 0, 0, kQScale, static_cast<uint16_t*>(tiles), n_tp, row_end, t0, t1 - t0,
-                  nullptr, 0, 0, ctx->err};
+                  nullptr, 0, 0, ctx->err, row_begin};
     return launch(ctx, ctx->prefill_pack[0][dt].at(n_kv_head), (unsigned)blocks, 1, 256, (hipStream_t)stream, &a);
 }
 
@@ -1326,7 +1333,7 @@ int tmac_attention_prefill_tiles(tmac_context* ctx, tmac_stream stream, const fl
     const int n_qblk = (n_q + kPrefillQueries - 1) / kPrefillQueries;
     PrefillArgs a{q, nullptr, nullptr, out, 0, n_q, prefix_len, n_qblk, kQScale,
                   static_cast<uint16_t*>(const_cast<void*>(tiles)), prefill_tiles_per_head(capacity),
-                  prefix_len + n_q, 0, 0, nullptr, 0, 0, ctx->err};
+                  prefix_len + n_q, 0, 0, nullptr, 0, 0, ctx->err, 0};
     return launch(ctx, it->second, (unsigned)((int64_t)n_qblk * n_kv_head * n_seq), 1, kPrefillWaves * 64,
                   (hipStream_t)stream, &a);
 }
