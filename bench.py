@@ -14,7 +14,8 @@ replayed for positions 0..255), config 4 ragged split-KV GB/s.
 
 The cpu_baseline leg times the reference CPU path restated in oracle/ (the
 -O3 build, one thread) on a sample of the config-3 batch and, as the checker,
-compares the GPU output of those sequences with it.
+compares the GPU output of those sequences with it; it also times configs 1
+and 2 (batch 1, the reference's own regime) on one thread.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 Prints ONE JSON line on stdout; progress goes to stderr.
@@ -62,7 +63,7 @@ def algo_bytes(lengths) -> int:
 SECTION_WARM_MS = 200.0
 
 
-def time_launches(ctx, stream, fn, steps: int, warmup: int, min_warm_ms: float = SECTION_WARM_MS):
+def time_launches(ctx, stream, fn, steps: int, warmup: int, min_warm_ms: float = SECTION_WARM_MS, stats=None):
     """Runs fn() `warmup` times untimed, and more in batches of 20 until at
     least `min_warm_ms` of wall time has passed since the first, then exactly
     `steps` times between two HIP events recorded on `stream` (synchronized
@@ -70,15 +71,22 @@ def time_launches(ctx, stream, fn, steps: int, warmup: int, min_warm_ms: float =
     instrumented pass of `steps` launches with an event after each gives the
     per-launch times for the percentiles (an event per launch adds ~2.6 us per
     launch at config 3, so it stays out of the mean).  Returns (per-launch ms,
-    mean ms)."""
+    mean ms); `stats` (a dict), when given, receives the untimed warm-up
+    launches done and their wall time."""
     t0 = time.perf_counter()
+    n_warm = 0
     for _ in range(warmup):
         fn()
+    n_warm += warmup
     ctx.synchronize(stream)
     while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
         for _ in range(20):
             fn()
+        n_warm += 20
         ctx.synchronize(stream)
+    if stats is not None:
+        stats["warmup_launches"] = n_warm
+        stats["warmup_ms"] = (time.perf_counter() - t0) * 1e3
     e0, e1 = ctx.event(), ctx.event()
     ctx.record(e0, stream)
     for _ in range(steps):
@@ -104,6 +112,14 @@ def pct(a, p):
     return float(np.percentile(a, p))
 
 
+# The headline's untimed warm-up: the requested --warmup launches, but at
+# least C3_MIN_WARM launches and SECTION_WARM_MS of sustained work (BASELINE.md
+# asks for >= 20 warm-ups; the clocks of an idle GPU take some tens of ms to
+# rise, and the first launches of a fresh process also pay first-touch costs).
+C3_MIN_WARM = 20
+COLD_SERIES = 100  # launches timed one by one from an idle GPU, before the warm-up
+
+
 def bench_c3(ctx, stream, steps, warmup, n_seq=256, n_pos=4096):
     log(f"[bench] C3: generating {n_seq}x{n_pos} fp32 K/V ({n_seq * n_pos * ROW_BYTES / 1e9:.2f} GB)")
     q, k, v = workloads.c3(n_seq, n_pos)
@@ -114,7 +130,20 @@ def bench_c3(ctx, stream, steps, warmup, n_seq=256, n_pos=4096):
     def launch():
         ctx.decode_batched(dq, dk, dv, dout, n_seq, NH, NKV, HD, n_pos, n_pos, stream=stream)
 
-    per, mean_ms = time_launches(ctx, stream, launch, steps, warmup, min_warm_ms=0.0)  # exactly W warm-up steps
+    # The first launches after the upload, one event pair each (part of the
+    # warm-up): how long the launch takes to settle from an idle GPU.
+    ctx.synchronize(stream)
+    evs = [ctx.event() for _ in range(COLD_SERIES + 1)]
+    ctx.record(evs[0], stream)
+    for i in range(COLD_SERIES):
+        launch()
+        ctx.record(evs[i + 1], stream)
+    ctx.synchronize(stream)
+    cold = np.array([ctx.elapsed_ms(evs[i], evs[i + 1]) for i in range(COLD_SERIES)]) * 1e3
+    for e in evs:
+        ctx.destroy_event(e)
+    stats = {}
+    per, mean_ms = time_launches(ctx, stream, launch, steps, max(warmup, C3_MIN_WARM), stats=stats)
     out = dout.numpy(stream)
     nbytes = algo_bytes(np.full(n_seq, n_pos))
     res = {
@@ -126,6 +155,14 @@ def bench_c3(ctx, stream, steps, warmup, n_seq=256, n_pos=4096):
         "gbs": nbytes / (mean_ms * 1e-3) / 1e9,
         "split_len": split_len,
         "n_splits": n_splits,
+        "warmup_launches": stats["warmup_launches"] + COLD_SERIES,
+        "warmup_ms": stats["warmup_ms"],
+        "cold_series_us": {
+            "first_10": [round(float(x), 1) for x in cold[:10]],
+            "mean_per_10": [round(float(cold[i:i + 10].mean()), 1) for i in range(0, COLD_SERIES, 10)],
+            "note": f"the first {COLD_SERIES} launches after the inputs were uploaded, each between two "
+                    "events (~2.6 us of event cost included), before the untimed warm-up",
+        },
     }
     for d in (dq, dk, dv, dout):
         d.free()
@@ -293,6 +330,9 @@ def bench_c2(ctx, stream, layers=24, cap=256, use_graph=True):
     return res
 
 
+C2_SWEEPS = 7  # timed sweeps over positions 0..255; each position's median is reported
+
+
 def c2_graph(ctx, stream, layer, pos, layers, cap):
     ctx.step_begin(stream)
     for i in range(layers):
@@ -314,15 +354,17 @@ def c2_graph(ctx, stream, layer, pos, layers, cap):
         return per
 
     sweep()  # warm-up sweep
-    per = np.stack([sweep() for _ in range(3)]).min(axis=0)
+    per = np.median(np.stack([sweep() for _ in range(C2_SWEEPS)]), axis=0)
     ctx.graph_destroy(g)
     step_bytes = [layers * (1024 * s + 9216) for s in range(1, cap + 1)]
     return {"median_step_us": float(np.median(per)), "p90_step_us": pct(per, 90),
             "p10_step_us": pct(per, 10), "max_step_us": float(per.max()),
             "step_us_s1": float(per[0]), "step_us_s128": float(per[127]),
             "step_us_s256": float(per[-1]),
-            "gbs_s256": step_bytes[-1] / (per[-1] * 1e-6) / 1e9,
-            "nodes_per_step": layers + 1}
+            "gbs_s256": float(step_bytes[-1] / (per[-1] * 1e-6) / 1e9),
+            "nodes_per_step": layers + 1, "sweeps": C2_SWEEPS,
+            "statistic": f"each position's median over {C2_SWEEPS} sweeps (after one untimed sweep) of its "
+                         "replay time between two events; median / p10 / p90 / max over the 256 positions"}
 
 
 def bench_c4(ctx, stream, steps, warmup, n_seq=16, max_len=32768):
@@ -446,6 +488,85 @@ def bench_qkv(ctx, stream, steps, warmup, layers=24, sets=16):
             "stream_weight_bytes": per_layer * n_inst}
 
 
+def bench_attn_block(ctx, stream, layers=24, cap=256, sweeps=5):
+    """The attention block of a decode step as one captured graph: per layer
+    tmac_fused_qkv_bias (Q5_0 q/k, Q8_0 v, biases) -> tmac_layer_attention_devpos
+    -> tmac_matmul_add (Q5_0 896 x 896 output projection + residual), then the
+    position advance (3 * layers + 1 nodes), replayed for positions 0..cap-1;
+    each position's median over `sweeps` sweeps."""
+    nq, nk, nv, cols = QKV_SHAPE
+    nb = cols // 32
+    rng = np.random.default_rng(24)
+
+    def blocks(rows, bb):
+        raw = rng.integers(0, 256, (rows * nb, bb), dtype=np.uint8)
+        raw[:, 0:2] = (rng.uniform(0.0005, 0.004, rows * nb).astype(np.float16)).view(np.uint8).reshape(-1, 2)
+        return raw.reshape(-1)
+
+    bq5, bk5, bv8, bo5 = nq * nb * 22, nk * nb * 22, nv * nb * 34, nq * nb * 22
+    dwq = ctx.upload(np.concatenate([blocks(nq, 22) for _ in range(layers)]))
+    dwk = ctx.upload(np.concatenate([blocks(nk, 22) for _ in range(layers)]))
+    dwv = ctx.upload(np.concatenate([blocks(nv, 34) for _ in range(layers)]))
+    dwo = ctx.upload(np.concatenate([blocks(nq, 22) for _ in range(layers)]))
+    db = [ctx.upload(rng.standard_normal(layers * n).astype(np.float32) * 0.1) for n in (nq, nk, nv)]
+    dx = ctx.upload(rng.standard_normal((layers, cols)).astype(np.float32))
+    dq, dk, dv = ctx.empty((layers, nq)), ctx.empty((layers, nk)), ctx.empty((layers, nv))
+    dctx = ctx.empty((layers, nq))
+    dh = ctx.upload(rng.standard_normal(nq).astype(np.float32))
+    kc, vc = ctx.empty((layers, cap, KVD)), ctx.empty((layers, cap, KVD))
+    kc.fill_bytes(0, stream)
+    vc.fill_bytes(0, stream)
+    pos = ctx.upload(np.zeros(1, np.int32))
+    ctx.rope_prepare(HD, 1e6, cap)
+
+    def layer(i):
+        ctx.fused_qkv(dwq.ptr + i * bq5, dwk.ptr + i * bk5, dwv.ptr + i * bv8, dx.at(i * cols), dq.at(i * nq),
+                      dk.at(i * nk), dv.at(i * nv), nq, nk, nv, cols, True, b_q=db[0].at(i * nq),
+                      b_k=db[1].at(i * nk), b_v=db[2].at(i * nv), stream=stream)
+        ctx.layer_attention_devpos(dq.at(i * nq), dk.at(i * nk), dv.at(i * nv), kc.at(i * cap * KVD),
+                                   vc.at(i * cap * KVD), dctx.at(i * nq), NH, NKV, HD, pos, cap, 1e6, stream=stream)
+        ctx.matmul(tmac_attn.TMAC_Q5_0, nq, cols, dwo.ptr + i * bo5, dctx.at(i * nq), dh, accumulate=True,
+                   stream=stream)
+
+    layer(0)
+    ctx.synchronize(stream)
+    ctx.step_begin(stream)
+    for i in range(layers):
+        layer(i)
+    ctx.pos_update(pos, 1, add=True, stream=stream)
+    g = ctx.step_end(stream)
+
+    def sweep():
+        ctx.pos_update(pos, 0, add=False, stream=stream)
+        evs = [ctx.event() for _ in range(cap + 1)]
+        ctx.record(evs[0], stream)
+        for st in range(cap):
+            ctx.graph_launch(g, stream)
+            ctx.record(evs[st + 1], stream)
+        ctx.synchronize(stream)
+        per = np.array([ctx.elapsed_ms(evs[i], evs[i + 1]) for i in range(cap)]) * 1e3
+        for e in evs:
+            ctx.destroy_event(e)
+        return per
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < SECTION_WARM_MS:
+        sweep()
+    per = np.median(np.stack([sweep() for _ in range(sweeps)]), axis=0)
+    ctx.graph_destroy(g)
+    assert ctx.check_device_error() == 0
+    for d in [dwq, dwk, dwv, dwo, dx, dq, dk, dv, dctx, dh, kc, vc, pos] + db:
+        d.free()
+    weights = layers * (bq5 + bk5 + bv8 + bo5)
+    act = layers * (cols * 4 + (nq + nk + nv) * 4 * 2 + nq * 4 * 2) + nq * 4 * 2  # bias, x, q/k/v, ctx, hidden
+    return {"median_step_us": float(np.median(per)), "p90_step_us": pct(per, 90), "max_step_us": float(per.max()),
+            "step_us_s1": float(per[0]), "step_us_s128": float(per[127]), "step_us_s256": float(per[-1]),
+            "weight_bytes_per_step": weights, "kv_bytes_per_step_s256": layers * (1024 * cap + 512),
+            "activation_bytes_per_step": act, "nodes_per_step": 3 * layers + 1, "sweeps": sweeps,
+            "note": "per layer: QKV projection + biases, fused RoPE + cache write + attention, output projection + "
+                    "residual; each position's median over the sweeps of its replay time between two events"}
+
+
 def bench_c5(ctx, stream, steps, warmup, n_seq=4, n_q=512, prefix=1536):
     """Config 5: chunked causal prefill on bf16 MFMA."""
     cap = prefix + n_q
@@ -531,6 +652,40 @@ def _median_of(fn, reps: int):
     return float(np.median(times)), times, res
 
 
+def cpu_batch1(oracle, reps: int = 5, c2_sweeps: int = 3):
+    """The reference CPU path at batch 1, its own regime (oracle timing build, one
+    thread): config 1 (attention_op at past_len 255) and config 2 (the 24-layer
+    step: RoPE + cache write + attention per layer, every position 0..255)."""
+    q, k, v = workloads.c1()
+    n = 200  # calls per timed run, issued as one oracle call over the same 256 rows
+    qn = np.repeat(q[None], n, axis=0)
+    offs, lens = np.zeros(n, np.int64), np.full(n, 256, np.int32)
+    sec, times, _ = _median_of(lambda: oracle.attention_ragged(qn, k, v, offs, lens, NH, NKV, HD, n_threads=1,
+                                                               timing=True), reps)
+    c1 = {"value": sec / n * 1e6, "unit": "us/call", "cores": 1, "kind": "port",
+          "sample": f"config 1 (14/2 heads, 256 rows, past_len 255): {n} calls per run, median of {reps} runs "
+                    "after 1 warm-up",
+          "run_s": [round(t, 5) for t in times]}
+    layers, cap = 24, 256
+    qs, kns, vns = workloads.c2(layers, cap)
+    per = np.empty((c2_sweeps, cap))
+    for sw in range(c2_sweeps + 1):  # the first sweep untimed
+        kc = np.zeros((layers, cap, KVD), np.float32)
+        vc = np.zeros((layers, cap, KVD), np.float32)
+        for st in range(cap):
+            t0 = time.perf_counter()
+            oracle.decode_step(qs[st], kns[st], vns[st], kc, vc, NH, NKV, HD, st, 1e6, timing=True)
+            if sw:
+                per[sw - 1, st] = time.perf_counter() - t0
+    per = np.median(per, axis=0) * 1e6
+    c2 = {"value": float(np.median(per)), "unit": "us/step", "cores": 1, "kind": "port",
+          "step_us_s1": float(per[0]), "step_us_s128": float(per[127]), "step_us_s256": float(per[-1]),
+          "sample": f"config 2: the 24-layer step (RoPE + cache write + attention per layer) at every position "
+                    f"0..255 of zeroed caches, each position's median over {c2_sweeps} sweeps after 1 untimed "
+                    "sweep; value = median over positions"}
+    return c1, c2
+
+
 def cpu_baseline(c3_data, budget_s: float = 12.0, reps: int = 5):
     """The reference CPU attention path (oracle/, -O3 build, one thread) timed
     on a sample of the config-3 batch (1 warm-up + `reps` timed runs, median);
@@ -564,6 +719,7 @@ def cpu_baseline(c3_data, budget_s: float = 12.0, reps: int = 5):
                                        timing=True)
 
     sec_mt, mt, _ = _median_of(multi, reps)
+    c1, c2 = cpu_batch1(oracle, reps)
     # checker: parity build (-ffp-contract=off) on every config-3 sequence
     chk = oracle.attention_ragged(q, k, v, offs, lens, NH, NKV, HD, n_threads=n_thr)
     err = np.abs(gpu_out.astype(np.float64) - chk)
@@ -584,6 +740,8 @@ def cpu_baseline(c3_data, budget_s: float = 12.0, reps: int = 5):
                       "sample": f"{n_mt} sequences, median of {reps} timed runs after 1 warm-up, OpenMP over "
                                 f"(sequence, head)",
                       "run_s": [round(t, 4) for t in mt]},
+        "c1": c1,
+        "c2": c2,
         "cpu_model": facts.get("model name", ""),
         "cpuinfo": facts,
         "nproc": usable,
@@ -606,8 +764,9 @@ def main():
     ap.add_argument("--target-groups", type=int, default=None, help="override TMAC_OPT_TARGET_GROUPS (tuning)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run plain 256 MiB device-to-device copies (counter calibration)")
-    ap.add_argument("--sections", default="c1,c2,c4,c5,qkv,kv,paged,ragged",
-                    help="extra sections to run besides config 3: any of c1,c2,c2eager,c4,c5,qkv,kv (bf16, "
+    ap.add_argument("--sections", default="c1,c2,block,c4,c5,qkv,kv,paged,ragged",
+                    help="extra sections to run besides config 3: any of c1,c2,c2eager,block (the attention "
+                         "block: QKV + layer attention + output projection, 24 layers),c4,c5,qkv,kv (bf16, "
                          "fp16, Q8_0 caches), kv16 (bf16, fp16 only), paged, ragged (256 sequences of "
                          "U[1, 4096] rows and a 64-sequence paged layer step, both fp32 schedules)")
     args = ap.parse_args()
@@ -655,6 +814,11 @@ def main():
     if "c2" in sections or "c2eager" in sections:
         extra["c2"] = bench_c2(ctx, stream, use_graph="c2" in sections)
         log(f"[bench] C2 {extra['c2']}")
+    if "block" in sections:
+        extra["attn_block"] = bench_attn_block(ctx, stream)
+        b = extra["attn_block"]
+        log(f"[bench] attention block (24 layers, {b['nodes_per_step']} nodes): median {b['median_step_us']:.1f} us, "
+            f"s=1 {b['step_us_s1']:.1f}, s=256 {b['step_us_s256']:.1f} us per step")
     if "c4" in sections:
         extra["c4"] = bench_c4(ctx, stream, max(10, args.steps // 2), args.warmup)
         log(f"[bench] C4 {extra['c4']['gbs']:.1f} GB/s")
@@ -739,6 +903,9 @@ def main():
             "n_seq": 256, "n_pos": 4096, "n_head": NH, "n_kv_head": NKV, "head_dim": HD,
             "split_len": c3["split_len"], "n_splits": c3["n_splits"],
         },
+        "warmup_launches": c3["warmup_launches"],
+        "warmup_ms": round(c3["warmup_ms"], 1),
+        "c3_cold_series_us": c3["cold_series_us"],
         "pct_of_peak": round(gbs / HBM_PEAK_GBS * 100, 2),
         "us_per_call": round(c3["mean_ms"] * 1e3, 2),
         "us_per_call_median": round(c3["median_ms"] * 1e3, 2),

@@ -70,6 +70,8 @@ def _load(path: str) -> ctypes.CDLL:
     lib.oracle_attention.restype = ctypes.c_int
     lib.oracle_layer_step.argtypes = [_F, _F, _F, _F, _F, _F] + [ctypes.c_int] * 4 + [ctypes.c_float]
     lib.oracle_layer_step.restype = ctypes.c_int
+    lib.oracle_decode_step.argtypes = [_F] * 6 + [ctypes.c_int] * 6 + [ctypes.c_float]
+    lib.oracle_decode_step.restype = ctypes.c_int
     lib.oracle_attention_ragged.argtypes = [_F, _F, _F, _I64, _I32, _F] + [ctypes.c_int] * 5
     lib.oracle_attention_ragged.restype = ctypes.c_int
     lib.oracle_prefill.argtypes = [_F, _F, _F, _F] + [ctypes.c_int] * 8
@@ -187,6 +189,24 @@ def layer_step(q, k_new, v_new, k_cache: np.ndarray, v_cache: np.ndarray, n_head
     if rc != 0:
         raise ValueError("oracle_layer_step: bad arguments")
     return out, q, k
+
+
+def decode_step(q, k_new, v_new, k_cache: np.ndarray, v_cache: np.ndarray, n_head: int, n_kv_head: int,
+                head_dim: int, pos: int, base: float = 1e6, timing: bool = False) -> np.ndarray:
+    """One decode step over every layer: q [L][n_head*hd], k_new / v_new [L][kdim], caches
+    [L][capacity][kdim] (updated in place).  Returns out [L][n_head*hd]."""
+    q = _f32(q).copy()
+    k = _f32(k_new).copy()
+    v = _f32(v_new)
+    n_layers, capacity = k_cache.shape[0], k_cache.shape[1]
+    assert k_cache.dtype == np.float32 and k_cache.flags["C_CONTIGUOUS"] and k_cache.shape == v_cache.shape
+    assert v_cache.dtype == np.float32 and v_cache.flags["C_CONTIGUOUS"]
+    out = np.empty((n_layers, n_head * head_dim), dtype=np.float32)
+    rc = lib(timing).oracle_decode_step(_fp(q), _fp(k), _fp(v), _fp(k_cache), _fp(v_cache), _fp(out), n_layers,
+                                        capacity, n_head, n_kv_head, head_dim, pos, base)
+    if rc != 0:
+        raise ValueError("oracle_decode_step: bad arguments")
+    return out
 
 
 def attention_ragged(q, k_pool, v_pool, offsets, lengths, n_head: int, n_kv_head: int,

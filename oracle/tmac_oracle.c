@@ -183,6 +183,26 @@ int oracle_layer_step(float* q, float* k_new, const float* v_new,
                             n_head, n_kv_head, head_dim, pos);
 }
 
+/* One decode step of the attention slice over n_layers layers, as the
+ * reference's per-layer loop runs it (tmac_gguf.cpp:1537-1568 around
+ * forward_layer_with_cache): layer l takes q + l*n_head*hd, k_new / v_new +
+ * l*kdim, its cache at + l*capacity*kdim, and writes out + l*n_head*hd.
+ * q and k_new are rotated in place. */
+int oracle_decode_step(float* q, float* k_new, const float* v_new, float* k_cache, float* v_cache,
+                       float* out, int n_layers, int capacity, int n_head, int n_kv_head, int head_dim,
+                       int pos, float base) {
+    if (n_layers < 1 || capacity < 1 || pos >= capacity) return -1;
+    const size_t qd = (size_t)n_head * head_dim, kdim = (size_t)n_kv_head * head_dim;
+    for (int l = 0; l < n_layers; l++) {
+        const int rc = oracle_layer_step(q + l * qd, k_new + l * kdim, v_new + l * kdim,
+                                         k_cache + (size_t)l * capacity * kdim,
+                                         v_cache + (size_t)l * capacity * kdim, out + l * qd, n_head,
+                                         n_kv_head, head_dim, pos, base);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 int oracle_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

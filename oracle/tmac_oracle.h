@@ -82,6 +82,12 @@ int oracle_layer_step(float* q, float* k_new, const float* v_new,
  * of the packed k/v pools and attends to all of them (past_len = lengths[s]-1).
  * q/out are [n_seq][n_head][head_dim].  n_threads > 1 runs (seq, head) pairs on
  * OpenMP threads; each pair is computed exactly as in the serial loop. */
+/* A decode step over n_layers layers (the reference's per-layer loop,
+ * tmac_gguf.cpp:1537-1568): oracle_layer_step for each layer in turn; layer
+ * l's cache starts l * capacity rows in. */
+int oracle_decode_step(float* q, float* k_new, const float* v_new, float* k_cache, float* v_cache,
+                       float* out, int n_layers, int capacity, int n_head, int n_kv_head, int head_dim,
+                       int pos, float base);
 int oracle_attention_ragged(const float* q, const float* k_pool, const float* v_pool,
                             const int64_t* offsets, const int32_t* lengths, float* out,
                             int n_seq, int n_head, int n_kv_head, int head_dim, int n_threads);

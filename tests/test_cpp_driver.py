@@ -1,7 +1,8 @@
 """Runs the C++ drivers under tests/cpp (built by __graft_entry__.build()): the
-reference's per-layer attention sequence driven through the hip_backend C++
-mirror, and a paged Q8_0 serving loop driven through the C ABI, each checked
-against the oracle for every layer of every step."""
+reference's per-layer attention block (QKV projection + biases, RoPE, cache
+write, attention, output projection + residual) driven through the hip_backend
+C++ mirror, per op and fused, and a paged Q8_0 serving loop driven through the C
+ABI, each checked against the oracle for every layer of every step."""
 import os
 import subprocess
 

@@ -257,6 +257,31 @@ def test_layer_step_is_rope_then_write_then_attention():
     np.testing.assert_array_equal(out, oracle.attention(q2, kc, vc, NH, NKV, HD, pos))
 
 
+def test_decode_step_equals_layer_steps_in_turn():
+    """The whole-step driver (the reference's per-layer loop) equals one
+    layer_step per layer, each on its own cache slice, bit for bit; the timing
+    build gives the same result within the fp32 bar."""
+    L, cap, pos = 3, 20, 13
+    kc = oracle.normal(61, (L, cap, NKV * HD))
+    vc = oracle.normal(62, (L, cap, NKV * HD))
+    q = oracle.normal(63, (L, NH * HD))
+    kn = oracle.normal(64, (L, NKV * HD))
+    vn = oracle.normal(65, (L, NKV * HD))
+    k1, v1 = kc.copy(), vc.copy()
+    out = oracle.decode_step(q, kn, vn, k1, v1, NH, NKV, HD, pos)
+    for layer in range(L):
+        k2, v2 = kc[layer].copy(), vc[layer].copy()
+        ref, _, _ = oracle.layer_step(q[layer], kn[layer], vn[layer], k2, v2, NH, NKV, HD, pos)
+        np.testing.assert_array_equal(out[layer], ref)
+        np.testing.assert_array_equal(k1[layer], k2)
+        np.testing.assert_array_equal(v1[layer], v2)
+    k3, v3 = kc.copy(), vc.copy()
+    out_t = oracle.decode_step(q, kn, vn, k3, v3, NH, NKV, HD, pos, timing=True)
+    assert np.all(np.abs(out_t - out) <= 2e-5 + 1e-4 * np.abs(out))
+    with pytest.raises(ValueError):
+        oracle.decode_step(q, kn, vn, kc.copy(), vc.copy(), NH, NKV, HD, cap)
+
+
 def test_ragged_driver_equals_single_sequence_calls():
     lens = np.array([1, 5, 40, 3], np.int32)
     offs = np.array([0, 1, 6, 46], np.int64)
