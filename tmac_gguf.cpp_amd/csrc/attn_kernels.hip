@@ -682,55 +682,102 @@ __device__ __forceinline__ bool seq_geometry(const DecodeArgs& a, int seq, int& 
 // rows fill the front of the grid (round-robin dispatch then spreads them
 // evenly over the XCDs) and surplus workgroups at the end exit.  Every wave
 // computes the same answer: lane l takes kScanPer consecutive sequences of a
-// round of 64 * kScanPer (their loads all in flight at once), and a 64-lane
-// inclusive scan of the lane sums finds the lane, then the sequence, holding
-// the unit.
+// round of 64 * kScanPer (their loads, and those of their `offsets` entries
+// when given, all in flight at once), and a 64-lane inclusive scan of the lane
+// sums finds the lane, then the sequence, holding the unit.  The sequence's
+// array value (raw) and offset come back with it, so the caller needs no
+// second round trip to memory before its K/V addresses are known.
 constexpr int kScanPer = 8;
-__device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths, int add, int n_seq,
-                                            int split_len, int n_splits, int unit, int& seq, int& split) {
+
+// Inclusive prefix sum over the 64 lanes: DPP row shifts inside each 16-lane
+// row, then the row totals read from lanes 15, 31 and 47.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1 (lanes shifted in add 0)
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
+    const int r2 = __builtin_amdgcn_readlane(x, 47);
+    const int row = (threadIdx.x & 63) >> 4;
+    return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
+__device__ __forceinline__ bool ragged_unit(const int32_t* __restrict__ lengths,
+                                            const int64_t* __restrict__ offsets, int add, int n_seq, int split_len,
+                                            int n_splits, int unit, int& seq, int& split, int& raw, int64_t& off) {
     const int lane = threadIdx.x & 63;
     int base = 0;
     for (int c0 = 0; c0 < n_seq; c0 += 64 * kScanPer) {
         const int s0 = c0 + lane * kScanPer;
+        int v[kScanPer];
+        int64_t o[kScanPer];
+#pragma unroll
+        for (int j = 0; j < kScanPer; ++j) {
+            const bool in = s0 + j < n_seq;
+            v[j] = in ? lengths[s0 + j] : 0;
+            o[j] = (in && offsets) ? offsets[s0 + j] : 0;
+        }
         int u[kScanPer];
         int sum = 0;
 #pragma unroll
         for (int j = 0; j < kScanPer; ++j) {
-            u[j] = 0;
-            if (s0 + j < n_seq) {
-                const long long len = (long long)lengths[s0 + j] + add;
-                u[j] = len > 0 ? (int)min((len + split_len - 1) / split_len, (long long)n_splits) : 1;
-            }
+            // rows L = v + add (add is 0 or 1, so L fits 32 unsigned bits); ceil(L / split_len), 1 for L <= 0
+            const int64_t len = (int64_t)v[j] + add;
+            unsigned uu = 1;
+            if (len > 0) uu = ((unsigned)len - 1u) / (unsigned)split_len + 1u;
+            u[j] = s0 + j < n_seq ? (int)min(uu, (unsigned)n_splits) : 0;
             sum += u[j];
         }
-        int incl = sum;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int t = __shfl_up(incl, off);
-            if (lane >= off) incl += t;
-        }
-        const int total = __builtin_amdgcn_readfirstlane(__shfl(incl, 63));  // uniform: keeps the loop's branches scalar
+        const int incl = wave_incl_scan(sum);
+        const int total = __builtin_amdgcn_readlane(incl, 63);
         if (unit < base + total) {
             const unsigned long long hit = __ballot(unit < base + incl);
-            const int first = __ffsll((long long)hit) - 1;
+            const int first = __builtin_amdgcn_readfirstlane(__ffsll((long long)hit) - 1);
             // Every lane resolves the unit inside its own sequences as if it
-            // were the hit lane; the hit lane's answer is broadcast.
-            int e = base + incl - sum, jj = 0, sp = 0;
+            // were the hit lane; the hit lane's answer is read out.
+            int e = base + incl - sum, jj = 0, sp = 0, vv = v[0];
+            int64_t oo = o[0];
 #pragma unroll
             for (int j = 0; j < kScanPer; ++j) {
                 if (unit >= e && unit < e + u[j]) {
                     jj = j;
                     sp = unit - e;
+                    vv = v[j];
+                    oo = o[j];
                 }
                 e += u[j];
             }
-            seq = __builtin_amdgcn_readfirstlane(__shfl(s0 + jj, first));
-            split = __builtin_amdgcn_readfirstlane(__shfl(sp, first));
-            return true;
+            seq = __builtin_amdgcn_readlane(s0 + jj, first);
+            split = __builtin_amdgcn_readlane(sp, first);
+            raw = __builtin_amdgcn_readlane(vv, first);
+            const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(uint32_t)oo, first);
+            const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)oo >> 32), first);
+            off = (int64_t)(((uint64_t)hi << 32) | lo);
+            return seq >= 0 && seq < n_seq && split >= 0 && split < n_splits;
         }
         base += total;
     }
     return false;
+}
+
+// Geometry of a unit-grid sequence from the values ragged_unit read:
+// raw = lengths[seq] (ragged, paged) or positions[seq] (paged layer).
+template <int MODE>
+__device__ __forceinline__ bool unit_geometry(const DecodeArgs& a, int raw, int64_t off, int& n_pos, int& pos,
+                                              size_t& base) {
+    pos = 0;
+    base = 0;
+    if (MODE == kRagged) {
+        n_pos = raw;
+        base = (size_t)off;
+    } else if (MODE == kPaged) {
+        n_pos = raw;
+    } else {
+        pos = raw;
+        if (pos < 0 || pos >= a.capacity || pos >= a.rope_rows) return false;
+        n_pos = pos + 1;
+    }
+    return true;
 }
 
 // Decode for one (split, sequence) workgroup.
@@ -757,16 +804,21 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     int split = PER_HEAD ? 0 : blockIdx.x;
     const int head = PER_HEAD ? blockIdx.x : 0;
     int seq = blockIdx.y;
-    if ((MODE == kRagged || PAGED) && !PER_HEAD) {  // grid = flat list of (sequence, split) units
-        const bool by_pos = MODE == kPagedLayer;
-        if (!ragged_unit(by_pos ? a.positions : a.lengths, by_pos ? 1 : 0, a.n_seq, a.split_len, a.n_splits,
-                         blockIdx.x, seq, split))
-            return;
-    }
-
     int n_pos, pos;
     size_t base;
-    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) {
+    bool geo_ok;
+    if ((MODE == kRagged || PAGED) && !PER_HEAD) {  // grid = flat list of (sequence, split) units
+        const bool by_pos = MODE == kPagedLayer;
+        int raw;
+        int64_t off;
+        if (!ragged_unit(by_pos ? a.positions : a.lengths, MODE == kRagged ? a.offsets : nullptr, by_pos ? 1 : 0,
+                         a.n_seq, a.split_len, a.n_splits, blockIdx.x, seq, split, raw, off))
+            return;
+        geo_ok = unit_geometry<MODE>(a, raw, off, n_pos, pos, base);
+    } else {
+        geo_ok = seq_geometry<MODE>(a, seq, n_pos, pos, base);
+    }
+    if (!geo_ok) {
         if (split == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
         return;
     }
@@ -3147,15 +3199,21 @@ __device__ __forceinline__ void mdecode_body(const DecodeArgs& a) {
     constexpr bool PAGED = is_paged(MODE);
     constexpr bool LAYER = is_layer(MODE);
     int split = blockIdx.x, seq = blockIdx.y;
-    if (MODE == kRagged || PAGED) {
-        const bool by_pos = MODE == kPagedLayer;
-        if (!ragged_unit(by_pos ? a.positions : a.lengths, by_pos ? 1 : 0, a.n_seq, a.split_len, a.n_splits,
-                         blockIdx.x, seq, split))
-            return;
-    }
     int n_pos, pos;
     size_t base;
-    if (!seq_geometry<MODE>(a, seq, n_pos, pos, base)) {
+    bool geo_ok;
+    if (MODE == kRagged || PAGED) {
+        const bool by_pos = MODE == kPagedLayer;
+        int raw;
+        int64_t off;
+        if (!ragged_unit(by_pos ? a.positions : a.lengths, MODE == kRagged ? a.offsets : nullptr, by_pos ? 1 : 0,
+                         a.n_seq, a.split_len, a.n_splits, blockIdx.x, seq, split, raw, off))
+            return;
+        geo_ok = unit_geometry<MODE>(a, raw, off, n_pos, pos, base);
+    } else {
+        geo_ok = seq_geometry<MODE>(a, seq, n_pos, pos, base);
+    }
+    if (!geo_ok) {
         if (split == 0 && threadIdx.x == 0) atomicOr(a.err, 1);
         return;
     }
