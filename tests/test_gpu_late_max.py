@@ -24,7 +24,9 @@ kTau` (the group kernel: C3 headline launch, C4 unit grid, stream-K; the head
 kernel), hv_body `sc - m > kTau` (split-V head kernel: attention_op at C1, the
 C2 layer step), any_body `mx - m > kTau` (any-shape kernel), prefill_body
 `(tm - m) * c > kTau` (C5), mdecode_segment's back() `tm - m > kTau` (MFMA
-decode of bf16 / fp16 / Q8_0 caches).  The reference's own GPU kernel fails on
+decode of bf16 / fp16 / Q8_0 caches); the same branches over paged caches
+(pages scattered in random pool order, planted rows on page boundaries) in the
+paged decode and the batched paged layer step.  The reference's own GPU kernel fails on
 exactly this class of input (kernel_flash_attn.metal:76-79).
 
 Oracle: oracle/tmac_oracle.c (tmac_gguf.cpp:990-1016, 1090-1091, 1093-1128).
@@ -437,4 +439,117 @@ def test_config5_prefill_late_max_all_rows(ctx):
         np.testing.assert_array_equal(ref[1, i], want)
         err = np.abs(got[1, i].astype(np.float64) - want)
         assert np.all(err <= 2.0 ** -21 * np.abs(want)), (i, float((err / np.abs(want)).max()))
+    assert ctx.check_device_error() == 0
+
+
+PAGED_DT = {"f32": tmac_attn.TMAC_KV_F32, "q8": tmac_attn.TMAC_KV_Q8_0}
+
+
+@pytest.mark.parametrize("dt", ["f32", "q8"])
+@pytest.mark.parametrize("stream_k", [0, 2])
+def test_paged_decode_late_max(ctx, dt, stream_k):
+    """Paged decode over 16-row pages scattered in random pool order -- the group
+    kernel (fp32 cache) and the MFMA kernel (Q8_0 cache), on the unit grid and on
+    stream-K -- with staircases across page boundaries (rows 15 | 16, 1023 | 1024)
+    up to the last row, a dominating row on a page boundary (row 2048; exact V), a
+    dominating last row, a raise at the last row, q x 30 and a gain ramp.  Oracle on
+    the rows gathered through the block table and widened to fp32."""
+    from test_gpu_kv_q8_paged import PR, build_pool, store, widen
+    code = PAGED_DT[dt]
+    lens = np.array([4096, 3000, 1537, 700, 64, 17], np.int32)
+    n_seq = lens.size
+    q = oracle.normal(8700, (n_seq, QD))
+    rows = [oracle.normal(8710 + s, (int(lens[s]), KVD)) for s in range(n_seq)]
+    vrows = [oracle.normal(8730 + s, (int(lens[s]), KVD)) for s in range(n_seq)]
+    rows[0] = lm.plant(q[0], rows[0], [15, 16, 1023, 1024, 4095], [9, 18, 27, 36, 45], NH, NKV, HD)
+    rows[1] = lm.plant(q[1], rows[1], [2048], [160], NH, NKV, HD)
+    rows[2] = lm.plant(q[2], rows[2], [1536], [9], NH, NKV, HD)
+    rows[3] = lm.plant(q[3], rows[3], [699], [160], NH, NKV, HD)
+    q[4] = q[4] * 30
+    rows[5] = lm.gain_ramp(rows[5], 3.0)
+    k_st = [store(r, code) for r in rows]
+    v_st = [store(r, code) for r in vrows]
+    n_pages = int(sum((l + PR - 1) // PR for l in lens)) + 7
+    kp, table = build_pool(k_st, code, n_pages, np.random.default_rng(87))
+    vp, _ = build_pool(v_st, code, n_pages, np.random.default_rng(87))
+    kw = [widen(r, code) for r in k_st]
+    vw = [widen(r, code) for r in v_st]
+    assert lm.dominance(q[1], kw[1], 2048, NH, NKV, HD) > 150
+    assert lm.dominance(q[3], kw[3], 699, NH, NKV, HD) > 150
+    dq, dk, dv, dtab, dl = ctx.upload(q), ctx.upload(kp), ctx.upload(vp), ctx.upload(table), ctx.upload(lens)
+    dout = ctx.empty((n_seq, QD))
+    ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, stream_k)
+    try:
+        ctx.decode_paged(dq, dk, dv, n_pages, dtab, table.shape[1], dl, dout, n_seq, NH, NKV, HD, int(lens.max()),
+                         total_rows=int(lens.sum()), kv_dtype=code)
+        got = dout.numpy()
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 1)
+    offs = np.concatenate([[0], np.cumsum(lens[:-1])]).astype(np.int64)
+    ref = oracle.attention_ragged(q, np.concatenate(kw), np.concatenate(vw), offs, lens, NH, NKV, HD, n_threads=8)
+    assert_close(got, ref, f"paged {dt} stream_k={stream_k}")
+    assert_v_row(got[1], vw[1][2048], f"paged {dt}: dominating row 2048")
+    assert_v_row(got[3], vw[3][699], f"paged {dt}: dominating last row")
+    for d in (dq, dk, dv, dtab, dl, dout):
+        d.free()
+    assert ctx.check_device_error() == 0
+
+
+@pytest.mark.parametrize("dt", ["f32", "q8"])
+@pytest.mark.parametrize("stream_k", [0, 2])
+def test_paged_layer_step_late_max(ctx, dt, stream_k):
+    """The batched paged layer step (RoPE, the new row written into its page,
+    attention over rows 0..pos): the new token of some sequences is planted 9 (and,
+    for one, 160) log2 units above every cached row, so the segment or split that
+    takes the new token raises its max on its last row; positions at and around
+    page boundaries.  Unit grid and stream-K (fp32); Q8_0 on the MFMA kernel."""
+    from test_gpu_kv_q8_paged import PR, build_pool, store, widen
+    code = PAGED_DT[dt]
+    positions = np.array([16, 1023, 2047, 300, 15, 999], np.int32)
+    levels = [9.0, 9.0, 160.0, 9.0, 9.0, None]
+    n_seq = positions.size
+    max_len = int(positions.max()) + 1
+    k_st = [store(oracle.normal(8800 + s, (int(p) + 1, KVD)), code) for s, p in enumerate(positions)]
+    v_st = [store(oracle.normal(8820 + s, (int(p) + 1, KVD)), code) for s, p in enumerate(positions)]
+    n_pages = int(sum((p + PR) // PR for p in positions)) + 5
+    kp, table = build_pool(k_st, code, n_pages, np.random.default_rng(88))
+    vp, _ = build_pool(v_st, code, n_pages, np.random.default_rng(88))
+    q = oracle.normal(8840, (n_seq, QD))
+    kn = oracle.normal(8841, (n_seq, KVD))
+    vn = oracle.normal(8842, (n_seq, KVD))
+    for s, (p, lev) in enumerate(zip(positions, levels)):
+        if lev is None:
+            continue
+        rows = np.array([table[s, r // PR] * PR + r % PR for r in range(int(p))])
+        q_rot = oracle.rope_heads(q[s], NH, HD, int(p), 1e6)
+        base = lm.scores_log2(q_rot, widen(kp[rows], code), NH, NKV, HD).max(axis=1)
+        qh = q[s].reshape(NH, HD)
+        for kv in range(NKV):
+            hs = slice(kv * G, (kv + 1) * G)
+            kn[s, kv * HD:(kv + 1) * HD] = lm.key_for_scores(qh[hs], kn[s, kv * HD:(kv + 1) * HD],
+                                                              base[hs] + lev, HD).astype(np.float32)
+    dq, dkn, dvn = ctx.upload(q), ctx.upload(kn), ctx.upload(vn)
+    dk, dv, dtab, dpos = ctx.upload(kp), ctx.upload(vp), ctx.upload(table), ctx.upload(positions)
+    dout = ctx.empty((n_seq, QD))
+    ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, stream_k)
+    try:
+        ctx.layer_attention_paged(dq, dkn, dvn, dk, dv, n_pages, dtab, table.shape[1], dpos, dout, n_seq, NH, NKV,
+                                  HD, max_len, 1e6, kv_dtype=code)
+        got, kp_got = dout.numpy(), dk.numpy()
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_STREAM_K, 1)
+    kp_ref, vp_ref = kp.copy(), vp.copy()
+    for s, p in enumerate(positions):
+        qr, kr = oracle.rope(q[s], kn[s], NH, NKV, HD, int(p), 1e6)
+        row = table[s, p // PR] * PR + p % PR
+        kp_ref[row] = store(kr, code)[0]
+        vp_ref[row] = store(vn[s], code)[0]
+        rows = np.array([table[s, r // PR] * PR + r % PR for r in range(int(p) + 1)])
+        ref = oracle.attention(qr, widen(kp_ref[rows], code), widen(vp_ref[rows], code), NH, NKV, HD, int(p))
+        assert_close(got[s], ref, f"paged layer {dt} stream_k={stream_k} seq {s} pos {p}")
+        if levels[s] is not None and levels[s] >= 150:
+            assert_v_row(got[s], widen(vp_ref[row:row + 1], code)[0], f"paged layer {dt}: dominating new token")
+    np.testing.assert_array_equal(kp_got, kp_ref)
+    for d in (dq, dkn, dvn, dk, dv, dtab, dpos, dout):
+        d.free()
     assert ctx.check_device_error() == 0

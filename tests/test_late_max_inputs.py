@@ -71,6 +71,21 @@ def test_planted_rows_rise_by_their_height():
     np.testing.assert_array_equal(kp[other], k[other])
 
 
+def test_planted_rows_survive_q8_storage():
+    """The staircase and the dominating row of the paged tests, after Q8_0 storage
+    (int8 per element, one fp16 scale per 32): each planted row still beats every row
+    before it by more than 8.5 log2 units, and the dominating row every other row by
+    more than 150, on the widened rows the kernels and the oracle read."""
+    q = oracle.normal(8700, (2, NH * HD))
+    k0 = lm.plant(q[0], oracle.normal(8710, (4096, NKV * HD)), [15, 16, 1023, 1024, 4095], [9, 18, 27, 36, 45],
+                  NH, NKV, HD)
+    k1 = lm.plant(q[1], oracle.normal(8711, (3000, NKV * HD)), [2048], [160], NH, NKV, HD)
+    w0 = oracle.q8_kv_widen(oracle.q8_kv_rows(k0.reshape(-1, HD))).reshape(k0.shape)
+    w1 = oracle.q8_kv_widen(oracle.q8_kv_rows(k1.reshape(-1, HD))).reshape(k1.shape)
+    assert np.all(lm.rise_margins(q[0], w0, [15, 16, 1023, 1024, 4095], NH, NKV, HD) > 8.5)
+    assert lm.dominance(q[1], w1, 2048, NH, NKV, HD) > 150
+
+
 @pytest.mark.parametrize("row", [0, 77, 255])
 def test_dominating_row_gives_its_v_exactly(row):
     q, k, v = c1_like(8200)
