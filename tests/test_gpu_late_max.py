@@ -40,6 +40,7 @@ import oracle
 import tmac_attn
 import workloads
 from conftest import assert_close
+from test_gpu_kv_q8_paged import PR, build_pool, store, widen
 
 pytestmark = pytest.mark.gpu
 NH, NKV, HD = 14, 2, 64
@@ -454,7 +455,6 @@ def test_paged_decode_late_max(ctx, dt, stream_k):
     up to the last row, a dominating row on a page boundary (row 2048; exact V), a
     dominating last row, a raise at the last row, q x 30 and a gain ramp.  Oracle on
     the rows gathered through the block table and widened to fp32."""
-    from test_gpu_kv_q8_paged import PR, build_pool, store, widen
     code = PAGED_DT[dt]
     lens = np.array([4096, 3000, 1537, 700, 64, 17], np.int32)
     n_seq = lens.size
@@ -503,7 +503,6 @@ def test_paged_layer_step_late_max(ctx, dt, stream_k):
     for one, 160) log2 units above every cached row, so the segment or split that
     takes the new token raises its max on its last row; positions at and around
     page boundaries.  Unit grid and stream-K (fp32); Q8_0 on the MFMA kernel."""
-    from test_gpu_kv_q8_paged import PR, build_pool, store, widen
     code = PAGED_DT[dt]
     positions = np.array([16, 1023, 2047, 300, 15, 999], np.int32)
     levels = [9.0, 9.0, 160.0, 9.0, 9.0, None]
