@@ -113,9 +113,10 @@ def pct(a, p):
 
 
 # The headline's untimed warm-up: the requested --warmup launches, but at
-# least C3_MIN_WARM launches and SECTION_WARM_MS of sustained work (BASELINE.md
-# asks for >= 20 warm-ups; the clocks of an idle GPU take some tens of ms to
-# rise, and the first launches of a fresh process also pay first-touch costs).
+# least C3_MIN_WARM launches and SECTION_WARM_MS of sustained work (at least 20
+# warm-ups before timing, as the reference's own benchmarks advise after 12,
+# BENCHMARKS.md:144-146; the clocks of an idle GPU take some tens of ms to rise,
+# and the first launches of a fresh process also pay first-touch costs).
 C3_MIN_WARM = 20
 COLD_SERIES = 100  # launches timed one by one from an idle GPU, before the warm-up
 

@@ -2,8 +2,8 @@
 
 Oracle: the reference's decode applied per query row (tmac_gguf.cpp:1093-1128
 with past_len = prefix + i), fed the bf16-rounded q/k/v the kernel computes
-with (config 5 compares against the oracle on bf16-rounded
-inputs).  Tolerance: the fp32 bound |gpu - ref| <= 2e-5 + 1e-4 |ref|.
+with (config 5 takes bf16 MFMA operands, so the parity inputs are the
+bf16-rounded ones).  Tolerance: the fp32 bound |gpu - ref| <= 2e-5 + 1e-4 |ref|.
 """
 import numpy as np
 import pytest
