@@ -68,7 +68,8 @@ enum tmac_status {
     TMAC_ERR_UNSUPPORTED = 4,     /* shape outside an entry point's domain (see Shapes), elem_op op 1 */
     TMAC_ERR_CAPACITY = 5,        /* position beyond the cache / RoPE table / workspace */
     TMAC_ERR_NOT_INITIALIZED = 6,
-    TMAC_ERR_CAPTURE = 7,         /* needs an allocation while the stream is being captured */
+    TMAC_ERR_CAPTURE = 7,         /* needs an allocation while the stream is being captured, or a device-wide
+                                     synchronize while a capture is in progress */
     TMAC_ERR_DEVICE_FAULT = 8,    /* a kernel reported a bad device-side position */
     TMAC_ERR_NOT_FOUND = 9,       /* no tensor of that name in a loaded weight file */
     TMAC_ERR_IO = 10,             /* weight file missing, truncated or not in TMAC format */
@@ -90,6 +91,11 @@ int tmac_abi_version(void);
  * on `device`, resolves every kernel, and allocates the split-KV workspace.
  * Fails with TMAC_ERR_HIP_BASE+... when no device or no gfx950 is present. */
 int tmac_init(tmac_context** ctx, int device);
+/* The caller's work on the context must be finished.  Contexts are independent: several may be used
+ * at the same time from different host threads (one thread per context at a time).  The library's own
+ * copies and fills run on a stream of the context, and it synchronizes the whole device only while no
+ * step capture of any context is in progress, so a call on one context never ends another thread's
+ * capture (on this runtime a legacy-stream copy or a device-wide synchronize from any thread would). */
 int tmac_shutdown(tmac_context* ctx);
 
 /* ---- the reference's three per-layer dispatches ---- */
@@ -414,8 +420,10 @@ int tmac_set_option(tmac_context* ctx, int option, int64_t value);
 int tmac_query_split(tmac_context* ctx, int n_seq, int n_pos, int n_head, int n_kv_head, int* split_len,
                      int* n_splits);
 /* Reads and clears the device error word (bit 0: bad device-side position, bit 1: ragged or paged length
- * above max_len, bit 2: block-table entry outside the page pool).
- * Synchronizes the context's device. Returns TMAC_ERR_DEVICE_FAULT if set. */
+ * above max_len, bit 2: block-table entry outside the page pool).  Returns TMAC_ERR_DEVICE_FAULT if set.
+ * Synchronizes the context's device first, unless a step capture (tmac_step_begin .. tmac_step_end) of any
+ * context is in progress: a device-wide synchronize would end that capture, so the word is then read as the
+ * kernels that have completed left it (synchronize the streams the work ran on before calling). */
 int tmac_check_device_error(tmac_context* ctx);
 
 /* ---- step capture: the analogue of metal_batch_begin / metal_batch_end
@@ -427,8 +435,10 @@ int tmac_step_begin(tmac_context* ctx, tmac_stream stream);
  * A graph keeps the addresses of the context's split-KV workspace and RoPE
  * tables that its captured launches used.  While any graph of the context is
  * alive, an eager call that needs a larger workspace or table allocates a new
- * one and keeps the old one allocated, so replays stay valid; the kept buffers
- * are freed when the context's last graph is destroyed, or at shutdown.
+ * one and keeps the old one allocated, so replays stay valid (so it does while
+ * a capture of any context is in progress, when the device cannot be
+ * synchronized); the kept buffers are freed when the context's last graph is
+ * destroyed and no capture is in progress, or at shutdown.
  * Graphs may outlive the context (destroying one later is safe), but must not
  * be launched after tmac_shutdown. */
 int tmac_step_end(tmac_context* ctx, tmac_stream stream, tmac_graph** graph);
@@ -447,6 +457,8 @@ int tmac_memset(tmac_context* ctx, tmac_stream stream, void* dst, int value, siz
 int tmac_stream_create(tmac_context* ctx, tmac_stream* stream);
 int tmac_stream_destroy(tmac_context* ctx, tmac_stream stream);
 int tmac_stream_synchronize(tmac_context* ctx, tmac_stream stream);
+/* TMAC_ERR_CAPTURE while a step capture of any context is in progress (a device-wide synchronize
+ * would end it): synchronize the streams instead. */
 int tmac_device_synchronize(tmac_context* ctx);
 typedef void* tmac_event;   /* hipEvent_t */
 int tmac_event_create(tmac_context* ctx, tmac_event* ev);

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdio>
@@ -126,6 +127,11 @@ struct tmac_context {
     float* ws = nullptr;
     size_t ws_floats = 0;
     int* err = nullptr;
+    // The library's own copies and fills (tables, tags, the error word) go on
+    // this non-blocking stream and wait for it alone: on this runtime a
+    // legacy-stream copy or a device-wide synchronize issued while a stream of
+    // another thread is capturing fails and ends that capture.
+    hipStream_t aux = nullptr;
     // RoPE row caches of the device-side position counters the layer entry
     // points have seen (kPosSlotBlocks blocks of kPosSlotBytes, allocated and
     // tagged empty at init); counters past the last block run without one.
@@ -206,6 +212,31 @@ bool capturing(hipStream_t s) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
     return st != hipStreamCaptureStatusNone;
+}
+
+// Step captures (tmac_step_begin .. tmac_step_end) in progress in any context
+// of the process.  While one is, no context synchronizes the whole device (a
+// device-wide synchronize from another thread fails and ends that capture):
+// buffers a growth replaces are retired instead of freed after a synchronize,
+// and the error check reads the error word without one.
+std::atomic<int> g_captures{0};
+
+// Synchronizes the context's device when no step capture is in progress;
+// true when the device is then idle.
+bool quiesce(tmac_context* ctx) {
+    if (g_captures.load() != 0) return false;
+    (void)hipSetDevice(ctx->device);
+    return hipDeviceSynchronize() == hipSuccess;
+}
+
+hipError_t aux_fill(tmac_context* ctx, void* p, int value, size_t bytes) {
+    hipError_t e = hipMemsetAsync(p, value, bytes, ctx->aux);
+    return e != hipSuccess ? e : hipStreamSynchronize(ctx->aux);
+}
+
+hipError_t aux_copy(tmac_context* ctx, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, ctx->aux);
+    return e != hipSuccess ? e : hipStreamSynchronize(ctx->aux);
 }
 
 struct Kernels {
@@ -359,11 +390,13 @@ struct FixedWorkspace {
     }
 };
 
-// Frees a device buffer the context no longer uses, or retires it while a
-// step graph that may have recorded its address is alive.
-void release_buffer(tmac_context* ctx, void* p) {
+// Frees a device buffer the context no longer uses (`idle`: the device was
+// synchronized, so no kernel still reads it), or retires it while a step graph
+// that may have recorded its address is alive or the device could not be
+// synchronized.
+void release_buffer(tmac_context* ctx, void* p, bool idle) {
     if (!p) return;
-    if (ctx->live_graphs > 0)
+    if (ctx->live_graphs > 0 || !idle)
         ctx->retired.push_back(p);
     else
         (void)hipFree(p);
@@ -379,12 +412,14 @@ void forget_graph(tmac_graph* g) {
     if (it != ctx->graphs.end()) ctx->graphs.erase(it);
 }
 
+// Frees the retired buffers once the device can be synchronized (otherwise
+// they wait for a later call, or shutdown).  A freed RoPE table's address may
+// come back for another table, so every row-cache tag is cleared with them.
 void free_retired(tmac_context* ctx) {
-    if (ctx->retired.empty()) return;
-    (void)hipSetDevice(ctx->device);
-    (void)hipDeviceSynchronize();
+    if (ctx->retired.empty() || !quiesce(ctx)) return;
     for (void* p : ctx->retired) (void)hipFree(p);
     ctx->retired.clear();
+    (void)aux_fill(ctx, ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes);
 }
 
 int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats) {
@@ -400,16 +435,14 @@ int ensure_workspace(tmac_context* ctx, hipStream_t stream, size_t floats) {
         return fail(ctx, TMAC_ERR_CAPTURE,
                     "split-KV workspace must grow but the stream is capturing; run the same shape once "
                     "before capture");
-    HIP_TRY(ctx, hipDeviceSynchronize());
-    if (floats > ctx->ws_floats) {
-        size_t n = ctx->ws_floats ? ctx->ws_floats : (1u << 20);
-        while (n < floats) n *= 2;
-        float* p = nullptr;
-        HIP_TRY(ctx, hipMalloc(&p, n * sizeof(float)));
-        release_buffer(ctx, ctx->ws);
-        ctx->ws = p;
-        ctx->ws_floats = n;
-    }
+    const bool idle = quiesce(ctx);
+    size_t n = ctx->ws_floats ? ctx->ws_floats : (1u << 20);
+    while (n < floats) n *= 2;
+    float* p = nullptr;
+    HIP_TRY(ctx, hipMalloc(&p, n * sizeof(float)));
+    release_buffer(ctx, ctx->ws, idle);
+    ctx->ws = p;
+    ctx->ws_floats = n;
     return TMAC_OK;
 }
 
@@ -452,18 +485,21 @@ int rope_table(tmac_context* ctx, hipStream_t stream, int head_dim, float base, 
         }
     }
     float2* dev = nullptr;
-    HIP_TRY(ctx, hipDeviceSynchronize());
+    const bool idle = quiesce(ctx);
     HIP_TRY(ctx, hipMalloc(&dev, host.size() * sizeof(float2)));
-    HIP_TRY(ctx, hipMemcpy(dev, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice));
-    // The position counters' RoPE row caches are tagged with table addresses;
-    // a new table may reuse a freed one's address, so every tag is cleared
-    // (the device is idle here).
-    HIP_TRY(ctx, hipMemset(ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes));
+    HIP_TRY(ctx, aux_copy(ctx, dev, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice));
+    // The position counters' RoPE row caches are tagged with table addresses,
+    // and a new table may reuse a freed one's address: with the device idle
+    // every tag is cleared.  Otherwise no table is freed (the old one is
+    // retired), so no address comes back and the tags stay (kernels may be
+    // reading them).
+    if (idle)
+        HIP_TRY(ctx, aux_fill(ctx, ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes));
     if (found) {
         // counters whose row caches tmac_pos_update refreshes from this table
         for (auto& pt : ctx->pos_table_of)
             if (pt.second.first == found->dev) pt.second = {dev, new_rows};
-        release_buffer(ctx, found->dev);
+        release_buffer(ctx, found->dev, idle);
         found->dev = dev;
         found->rows = new_rows;
     } else {
@@ -675,6 +711,11 @@ int tmac_init(tmac_context** out, int device) {
         return rc;
     }
     auto bail = [&](int rc) {
+        if (ctx->aux) (void)hipStreamSynchronize(ctx->aux);
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        if (ctx->err) (void)hipFree(ctx->err);
+        if (ctx->pos_slot_pool) (void)hipFree(ctx->pos_slot_pool);
+        if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
         for (auto& m : ctx->modules)
             if (m) (void)hipModuleUnload(m);
         delete ctx;
@@ -823,12 +864,15 @@ int tmac_init(tmac_context** out, int device) {
         (e = get_function(ctx, &ctx->k_kq, "tmac_matmul_kq")) != hipSuccess ||
         (e = get_function(ctx, &ctx->k_cvt_q8, "tmac_cvt_q8")) != hipSuccess)
         return bail(hip_fail(ctx, e, "hipModuleGetFunction"));
+    if ((e = hipStreamCreateWithFlags(&ctx->aux, hipStreamNonBlocking)) != hipSuccess)
+        return bail(hip_fail(ctx, e, "hipStreamCreateWithFlags"));
     if ((e = hipMalloc(&ctx->err, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMalloc"));
-    if ((e = hipMemset(ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemset"));
+    if ((e = aux_fill(ctx, ctx->err, 0, sizeof(int))) != hipSuccess) return bail(hip_fail(ctx, e, "hipMemsetAsync"));
     if ((e = hipMalloc(&ctx->pos_slot_pool, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes)) != hipSuccess)
         return bail(hip_fail(ctx, e, "hipMalloc"));
-    if ((e = hipMemset(ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes)) != hipSuccess)
-        return bail(hip_fail(ctx, e, "hipMemset"));  // every tag -1: no slot holds a row yet
+    if ((e = aux_fill(ctx, ctx->pos_slot_pool, 0xFF, (size_t)tmac::kPosSlotBlocks * tmac::kPosSlotBytes)) !=
+        hipSuccess)
+        return bail(hip_fail(ctx, e, "hipMemsetAsync"));  // every tag -1: no slot holds a row yet
     int rc = ensure_workspace(ctx, nullptr, (size_t)1 << 20);
     if (rc) return bail(rc);
     void* scratch = nullptr;
@@ -843,7 +887,10 @@ int tmac_shutdown(tmac_context* ctx) {
     if (!ctx) return TMAC_ERR_NOT_INITIALIZED;
     if (ctx->modules[0]) {
         (void)hipSetDevice(ctx->device);
-        (void)hipDeviceSynchronize();
+        // The caller has finished its work on this context; the device is
+        // synchronized as well unless a step capture is in progress somewhere.
+        (void)quiesce(ctx);
+        if (ctx->aux) (void)hipStreamSynchronize(ctx->aux);
         for (auto& t : ctx->rope) (void)hipFree(t.dev);
         if (ctx->ws) (void)hipFree(ctx->ws);
         for (void* p : ctx->retired) (void)hipFree(p);
@@ -853,6 +900,7 @@ int tmac_shutdown(tmac_context* ctx) {
         for (auto& m : ctx->modules)
             if (m) (void)hipModuleUnload(m);
     }
+    if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
     delete ctx;
     return TMAC_OK;
 }
@@ -1581,12 +1629,11 @@ int tmac_check_device_error(tmac_context* ctx) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
-    HIP_TRY(ctx, hipDeviceSynchronize());
+    (void)quiesce(ctx);
     int v = 0;
-    HIP_TRY(ctx, hipMemcpy(&v, ctx->err, sizeof(int), hipMemcpyDeviceToHost));
+    HIP_TRY(ctx, aux_copy(ctx, &v, ctx->err, sizeof(int), hipMemcpyDeviceToHost));
     if (v) {
-        HIP_TRY(ctx, hipMemset(ctx->err, 0, sizeof(int)));
-        HIP_TRY(ctx, hipDeviceSynchronize());
+        HIP_TRY(ctx, aux_fill(ctx, ctx->err, 0, sizeof(int)));
         return fail(ctx, TMAC_ERR_DEVICE_FAULT, "a kernel saw a device-side position outside its table or cache");
     }
     return TMAC_OK;
@@ -1598,6 +1645,7 @@ int tmac_step_begin(tmac_context* ctx, tmac_stream stream) {
     if (!stream) return fail(ctx, TMAC_ERR_INVALID_ARG, "step_begin: capture needs a created stream, not NULL");
     if ((rc = set_device(ctx))) return rc;
     HIP_TRY(ctx, hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    g_captures.fetch_add(1);
     return TMAC_OK;
 }
 
@@ -1606,7 +1654,10 @@ int tmac_step_end(tmac_context* ctx, tmac_stream stream, tmac_graph** graph) {
     if (rc) return rc;
     if (!graph) return fail(ctx, TMAC_ERR_NULL_POINTER, "step_end: null graph handle");
     hipGraph_t g = nullptr;
-    HIP_TRY(ctx, hipStreamEndCapture((hipStream_t)stream, &g));
+    const bool was_capturing = capturing((hipStream_t)stream);
+    const hipError_t ec = hipStreamEndCapture((hipStream_t)stream, &g);
+    if (was_capturing) g_captures.fetch_sub(1);
+    HIP_TRY(ctx, ec);
     if (*graph && (*graph)->exec) {
         hipGraphNode_t err_node = nullptr;
         hipGraphExecUpdateResult res;
@@ -1731,6 +1782,10 @@ int tmac_device_synchronize(tmac_context* ctx) {
     int rc = check_ctx(ctx);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
+    if (g_captures.load() != 0)
+        return fail(ctx, TMAC_ERR_CAPTURE,
+                    "device_synchronize: a step capture is in progress (a device-wide synchronize would end it); "
+                    "synchronize the streams instead");
     HIP_TRY(ctx, hipDeviceSynchronize());
     return TMAC_OK;
 }
@@ -1854,10 +1909,11 @@ int tmac_model_load(tmac_context* ctx, const char* path, tmac_model** model) {
             return fail(ctx, TMAC_ERR_IO, "model_load: cannot read tensor " + e.name);
         }
         if (m->on_device && e.n_bytes) {
-            const hipError_t err = hipMemcpy(m->blob + e.offset, staging.data(), e.n_bytes, hipMemcpyHostToDevice);
+            const hipError_t err = aux_copy(ctx, m->blob + e.offset, staging.data(), e.n_bytes,
+                                            hipMemcpyHostToDevice);
             if (err != hipSuccess) {
                 (void)hipFree(m->blob);
-                return hip_fail(ctx, err, "model_load: hipMemcpy");
+                return hip_fail(ctx, err, "model_load: hipMemcpyAsync");
             }
         }
     }
