@@ -27,6 +27,8 @@
  *    (NULL = the null stream).
  *  - A context is used from one host thread at a time, and its launches must
  *    not overlap on several streams (they share the split-KV workspace).
+ *    Different contexts are independent: each may be driven from its own
+ *    thread at the same time as the others (see tmac_shutdown).
  *  - Cache layout is the reference's: one row per position, row =
  *    [n_kv_head][head_dim] fp32 (tmac_gguf.cpp:200-201).
  *    Query head h reads kv head h / (n_head / n_kv_head) (tmac_gguf.cpp:1099).
