@@ -21,6 +21,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <numeric>
 #include <string>
 #include <unordered_map>
 #include <utility>
@@ -329,8 +330,11 @@ int check_shape(tmac_context* ctx, int n_head, int n_kv_head, int head_dim, Kern
 // knows it) the split length is total/target instead, so the workgroups that
 // actually have rows come close to one per CU whatever the length mix.
 void choose_split(const tmac_context* ctx, int waves, int n_seq, int n_pos, int n_kv_head, int* split_len,
-                  int* n_splits, int64_t total_rows = 0) {
-    const int round = waves * (kSlotsPerWave / n_kv_head);
+                  int* n_splits, int64_t total_rows = 0, int align = 1) {
+    // `align`: split lengths are also a multiple of it (paged caches: the
+    // 16-row page, which the MFMA decode's tiles and the group kernel's steps
+    // must not straddle).
+    const int round = std::lcm(waves * (kSlotsPerWave / n_kv_head), align);
     const int rounds = (n_pos + round - 1) / round;
     int len;
     const int64_t target_groups = ctx->opt_target_groups > 0 ? ctx->opt_target_groups : (int64_t)ctx->n_cu;
@@ -552,7 +556,8 @@ int run_decode(tmac_context* ctx, hipStream_t stream, const Kernels& k, DecodeAr
         waves = 4;
     }
     int split_len = 0, n_splits = 0;
-    choose_split(ctx, waves, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows);
+    choose_split(ctx, waves, n_seq, grid_rows, n_kv_head, &split_len, &n_splits, total_rows,
+                 a.block_table ? kPageRows : 1);
     a.split_len = split_len;
     a.n_splits = n_splits;
     if (n_splits > 1) {
