@@ -362,10 +362,12 @@ def c2_graph(ctx, stream, layer, pos, layers, cap):
             "p10_step_us": pct(per, 10), "max_step_us": float(per.max()),
             "step_us_s1": float(per[0]), "step_us_s128": float(per[127]),
             "step_us_s256": float(per[-1]),
+            "bins_us": [round(float(b), 2) for b in per.reshape(-1, 16).mean(axis=1)] if cap % 16 == 0 else None,
             "gbs_s256": float(step_bytes[-1] / (per[-1] * 1e-6) / 1e9),
             "nodes_per_step": layers + 1, "sweeps": C2_SWEEPS,
             "statistic": f"each position's median over {C2_SWEEPS} sweeps (after one untimed sweep) of its "
-                         "replay time between two events; median / p10 / p90 / max over the 256 positions"}
+                         "replay time between two events; median / p10 / p90 / max over the 256 positions; "
+                         "bins_us: mean over positions 16 b .. 16 b + 15"}
 
 
 def bench_c4(ctx, stream, steps, warmup, n_seq=16, max_len=32768):

@@ -1374,7 +1374,14 @@ __device__ __forceinline__ void hv_body(const DecodeArgs& a) {
     constexpr int PPS = kSlots;          // rows per step (one kv head)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int head = blockIdx.x / VS, vp = blockIdx.x % VS, seq = blockIdx.y;
+    // XCD-aware order: XCD x (= blockIdx.x % 8) takes a contiguous run of the
+    // logical order (kv head, V part, head in group), so the workgroups that
+    // read one kv head's K rows and one V part share an L2.
+    const int n_blk = gridDim.x, xcd = blockIdx.x & 7;
+    const int per = n_blk >> 3, rem = n_blk & 7;
+    const int logical = xcd * per + min(xcd, rem) + (blockIdx.x >> 3);
+    const int lt = logical / G;
+    const int vp = lt % VS, head = (lt / VS) * G + (logical - lt * G), seq = blockIdx.y;
     const int slot = lane / kLanesPerSlot, c = lane % kLanesPerSlot;
     const int kvh = head / G;
     const int vdim0 = hv_vdim0<VS>(vp, c);
