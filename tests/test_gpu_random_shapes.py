@@ -247,3 +247,59 @@ def test_paged_split_lengths_align_to_pages(ctx, dt, g, kv, split_len):
         for d in (dq, dk, dv, dtab, dl, out):
             d.free()
     assert ctx.check_device_error() == 0, what
+
+
+@pytest.mark.parametrize("vs", [1, 2, 4, 8])
+@pytest.mark.parametrize("g,kv", SHAPES)
+def test_split_v_every_shape_and_split(ctx, g, kv, vs):
+    """The split-V head kernel on every compiled shape and V split: its n_head * VS
+    workgroups are dealt to the XCDs in a remapped order (contiguous runs of
+    (kv head, V part, head in group) per XCD), which is a permutation of the grid
+    also when the grid is not a multiple of 8 (n_head * VS = 1, 2, 4, 7, 8, 14, 16,
+    28, ...).  attention_op on 1 and 300 rows, a ragged batch of two sequences
+    (one of them empty) and the fused layer step (new cache rows bit for bit)."""
+    nh, kvd = g * kv, kv * HD
+    what = f"g={g} kv={kv} vs={vs}"
+    ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_HEADV)
+    ctx.set_option(tmac_attn.TMAC_OPT_HV_SPLIT, vs)
+    dev = []
+
+    def up(x):
+        d = ctx.upload(x)
+        dev.append(d)
+        return d
+    try:
+        for past_len in (0, 299):
+            k, v = oracle.normal(8600 + past_len, (past_len + 1, kvd)), oracle.normal(8601 + past_len, (past_len + 1, kvd))
+            q = oracle.normal(8602 + past_len, nh * HD)
+            out = ctx.empty(nh * HD)
+            dev.append(out)
+            ctx.attention_op(up(q), up(k), up(v), out, nh, kv, HD, past_len)
+            assert_close(out.numpy(), oracle.attention(q, k, v, nh, kv, HD, past_len), f"{what} past_len {past_len}")
+        lens = np.array([0, 77], np.int32)
+        offs = np.array([0, 0], np.int64)
+        k, v = oracle.normal(8610, (77, kvd)), oracle.normal(8611, (77, kvd))
+        q = oracle.normal(8612, (2, nh * HD))
+        out = ctx.empty((2, nh * HD))
+        dev.append(out)
+        ctx.decode_ragged(up(q), up(k), up(v), up(offs), up(lens), out, 2, nh, kv, HD, 77)
+        got = out.numpy()
+        assert np.all(got[0] == 0), what
+        assert_close(got[1:], oracle.attention_ragged(q[1:], k, v, offs[1:], lens[1:], nh, kv, HD), what + " ragged")
+        pos, cap = 150, 160
+        kc, vc = oracle.normal(8620, (cap, kvd)), oracle.normal(8621, (cap, kvd))
+        q, kn, vn = oracle.normal(8622, nh * HD), oracle.normal(8623, kvd), oracle.normal(8624, kvd)
+        dkc, dvc, out = up(kc), up(vc), ctx.empty(nh * HD)
+        dev.append(out)
+        ctx.layer_attention(up(q), up(kn), up(vn), dkc, dvc, out, nh, kv, HD, pos, cap, 1e6)
+        kc_ref, vc_ref = kc.copy(), vc.copy()
+        ref, _, _ = oracle.layer_step(q, kn, vn, kc_ref, vc_ref, nh, kv, HD, pos, 1e6)  # updates the copies
+        assert_close(out.numpy(), ref, what + " layer step")
+        np.testing.assert_array_equal(dkc.numpy(), kc_ref, err_msg=what)
+        np.testing.assert_array_equal(dvc.numpy(), vc_ref, err_msg=what)
+    finally:
+        ctx.set_option(tmac_attn.TMAC_OPT_KERNEL, tmac_attn.TMAC_KERNEL_AUTO)
+        ctx.set_option(tmac_attn.TMAC_OPT_HV_SPLIT, 8)
+        for d in dev:
+            d.free()
+    assert ctx.check_device_error() == 0, what
