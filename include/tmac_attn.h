@@ -117,8 +117,9 @@ int tmac_rope_op(tmac_context* ctx, tmac_stream stream, float* data, int n_heads
                  int pos, float base);
 /* rope_op over n_rows rows (row r at data + r * row_stride floats, n_heads heads each) at positions
  * first_pos + r: the RoPE of a prompt chunk before its rows are written to the cache.  Row r is
- * bit-identical to tmac_rope_op at position first_pos + r.  No counterpart in the reference, which
- * feeds a prompt one token at a time (tmac_gguf.cpp:1621-1658). */
+ * bit-identical to tmac_rope_op at position first_pos + r.  data and every row are 16-byte aligned
+ * (row_stride a multiple of 4 floats; otherwise TMAC_ERR_MISALIGNED).  No counterpart in the reference,
+ * which feeds a prompt one token at a time (tmac_gguf.cpp:1621-1658). */
 int tmac_rope_rows(tmac_context* ctx, tmac_stream stream, float* data, int n_rows, int64_t row_stride, int n_heads,
                    int head_dim, int first_pos, float base);
 

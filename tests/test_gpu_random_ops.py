@@ -79,17 +79,23 @@ def test_random_qkv_integer_bit_exact(ctx, seed):
 @pytest.mark.parametrize("seed", range(16))
 def test_random_rope_rows_bit_exact(ctx, seed):
     """RoPE on n_rows rows at positions first_pos .. first_pos + n_rows - 1, rows
-    row_stride floats apart (the floats between rows are left alone)."""
+    row_stride floats apart (the floats between rows are left alone); a stride that
+    leaves rows off 16-byte alignment is refused before any launch."""
     rng = np.random.default_rng(11200 + seed)
     n_heads = int(rng.integers(1, 17))
     hd = int(rng.choice([2, 8, 32, 64, 64, 96, 128, 256]))
     n_rows = int(rng.integers(1, 40))
-    stride = n_heads * hd + int(rng.choice([0, 0, 4, 64]))
+    natural = n_heads * hd
+    stride = (natural + 3) // 4 * 4 + int(rng.choice([0, 0, 4, 64]))  # rows 16-byte aligned
     first = int(rng.choice([0, int(rng.integers(1, 100)), int(rng.integers(100, 30000))]))
     base = float(rng.choice([1e4, 1e6]))
     x = oracle.normal(11300 + seed, n_rows * stride)
     dx = ctx.upload(x)
     try:
+        if natural % 4:  # a row stride that is not 16-byte aligned is refused
+            with pytest.raises(tmac_attn.TmacError) as e:
+                ctx.rope_rows(dx, n_rows, natural, n_heads, hd, first, base)
+            assert e.value.status == tmac_attn.TMAC_ERR_MISALIGNED
         ctx.rope_rows(dx, n_rows, stride, n_heads, hd, first, base)
         got = dx.numpy()
     finally:
