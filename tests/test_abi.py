@@ -48,6 +48,46 @@ def test_calls_without_context_are_rejected():
     assert lib.tmac_shutdown(None) == nc
 
 
+
+# Entry points whose first argument is not a live context by design: the model
+# functions take a model handle (a model may be loaded without a context), and a
+# graph may be destroyed after its context is shut down.
+NO_CONTEXT = {"tmac_status_string", "tmac_last_error", "tmac_abi_version", "tmac_init", "tmac_synth_normal",
+              "tmac_synth_uniform", "tmac_prefill_tiles_bytes", "tmac_model_load", "tmac_model_count",
+              "tmac_model_tensor", "tmac_model_find", "tmac_model_free", "tmac_graph_destroy"}
+
+
+def _null_args(argtypes):
+    return [0.0 if a in (ctypes.c_float, ctypes.c_double)
+            else 0 if a in (ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_uint64)
+            else None for a in argtypes]
+
+
+def test_every_context_entry_point_rejects_a_null_context():
+    """Every entry point that takes a context returns TMAC_ERR_NOT_INITIALIZED for a
+    null one (every other argument null or zero), before it reads any argument."""
+    lib = tmac_attn.load_library()
+    checked = []
+    for name, (_, argtypes) in tmac_attn.SIGNATURES.items():
+        if name in NO_CONTEXT:
+            continue
+        assert argtypes and argtypes[0] is ctypes.c_void_p, name
+        assert getattr(lib, name)(*_null_args(argtypes)) == tmac_attn.TMAC_ERR_NOT_INITIALIZED, name
+        checked.append(name)
+    assert len(checked) >= 40
+
+
+def test_context_free_entry_points_on_null_handles():
+    """The documented exceptions: destroying a null graph or freeing a null model is a
+    no-op; the model queries report a null handle."""
+    lib = tmac_attn.load_library()
+    assert lib.tmac_graph_destroy(None, None) == tmac_attn.TMAC_OK
+    assert lib.tmac_model_free(None, None) == tmac_attn.TMAC_OK
+    assert lib.tmac_model_count(None) < 0
+    assert lib.tmac_model_load(None, None, None) == tmac_attn.TMAC_ERR_NULL_POINTER
+    assert lib.tmac_model_tensor(None, 0, None) == tmac_attn.TMAC_ERR_NULL_POINTER
+    assert lib.tmac_model_find(None, None, None) == tmac_attn.TMAC_ERR_NULL_POINTER
+
 def test_prefill_tiles_bytes():
     """16 KiB per 64-row tile and (sequence, kv head); rows rounded up to whole 4-tile stages."""
     lib = tmac_attn.load_library()
